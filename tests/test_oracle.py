@@ -1,0 +1,338 @@
+"""Pins the CPU oracle (oracle/cxm_oracle.c) before it is trusted as the
+parity checker of the HIP path.
+
+The reference ships no tests, golden vectors or fixtures (its tests/*.cpp are
+comment stubs), and its own reduce.cpp/broadcast.cpp/matrix.cpp cannot be
+compiled here without stand-ins for MSVC __forceinline, Intel SVML and TLX.
+So every oracle function is pinned by checks that do not retype its formula:
+
+* hand-derived known answers (tests/golden/kat_oracle.json) whose values only
+  come out right with the reference's exact fold/lane/panel order;
+* exact arithmetic: small-integer inputs, where every order gives the exact
+  integer sum, so a dropped tail, lane or panel shows;
+* library routines: numpy float32 elementwise ops (IEEE single rounding) and
+  float64 reductions/matmul; numpy's axis-0 float32 reduction, which adds
+  rows in order exactly like reduce.cpp:51-62;
+* brute force for max/argmax (order-free; first index wins on ties);
+* float64 torch answers for the compositions the reference lacks
+  (tests/golden/fixtures_f64.npz, written by tests/golden/make_fixtures.py);
+* closed forms and invariants (softmax rows sum to 1, constant rows give 1/N,
+  masked entries give exactly 0 / -inf).
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KAT = json.load(open(os.path.join(HERE, "golden", "kat_oracle.json")))
+FIX = np.load(os.path.join(HERE, "golden", "fixtures_f64.npz"))
+
+
+def f32(v):
+    return np.array(v, dtype=np.float32)
+
+
+def hexf(v: float) -> str:
+    return hex(int(np.float32(v).view(np.uint32)))
+
+
+def ulp_dist(a, b):
+    """Distance in units in the last place between float32 arrays."""
+    ai = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    bi = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    ai = np.where(ai < 0, -(ai & 0x7FFFFFFF), ai)
+    bi = np.where(bi < 0, -(bi & 0x7FFFFFFF), bi)
+    return np.abs(ai - bi)
+
+
+# ------------------------------------------------------------------ sum
+
+@pytest.mark.parametrize("case", KAT["sum_flat"], ids=lambda c: c["name"])
+def test_sum_flat_kat(orc, case):
+    # lane_fold_pairs: lanes (l, l+4) pair first: (2^24 + -2^24) + (1+1) + ... = 0+2+2+2 = 6;
+    #   a plain left-to-right sum gives 3 (each +1 after 2^24 rounds away).
+    # lanes_accumulate_across_blocks: lane 0 holds 2^24 + 1 -> 2^24 (ties to even),
+    #   lane 1 holds 1; fold: (2^24 + 1) + 0 -> 2^24.  Folding each block first gives 2^24 + 2.
+    # tail_added_after_fold: fold gives 2^24, each tail 1 rounds away; summing the tail
+    #   first (3) gives 2^24 + 4.
+    # short_is_sequential: 1 + 2^24 -> 2^24, + 1 -> 2^24; pairing the ones first gives 2^24 + 2.
+    z = orc.reduce_flat("sum", f32(case["x"]))
+    assert z[0] == np.float32(case["expect"])
+
+
+@pytest.mark.parametrize("n", [0, 1, 5, 7, 8, 9, 15, 16, 17, 63, 64, 65, 1000, 4099])
+def test_sum_flat_small_integers_exact(orc, n):
+    rng = np.random.default_rng(n)
+    x = rng.integers(-100, 101, size=n).astype(np.float32)
+    z = orc.reduce_flat("sum", x)
+    assert z[0] == np.float32(int(x.astype(np.int64).sum()))
+
+
+@pytest.mark.parametrize("n", [3, 8, 1000, 65537, 1 << 20])
+def test_sum_flat_vs_float64(orc, n):
+    rng = np.random.default_rng(100 + n)
+    x = rng.uniform(-1, 1, n).astype(np.float32)
+    z = orc.reduce_flat("sum", x)[0]
+    exact = np.sum(x.astype(np.float64))
+    # n/8 sequential adds per lane: error <= (n/8 + 3) * eps32 * sum|x|
+    bound = (n / 8 + 3) * 2.0 ** -24 * np.sum(np.abs(x.astype(np.float64)))
+    assert abs(float(z) - exact) <= bound
+
+
+@pytest.mark.parametrize("outer,dim,inner", [(1, 7, 3), (2, 5, 9), (1, 257, 33), (3, 64, 17), (1, 4, 4096)])
+def test_sum_axis_inner_matches_numpy_rowwise_order(orc, outer, dim, inner):
+    # numpy reduces axis 1 of a C-ordered [outer, dim, inner] array by adding
+    # slices d = 0, 1, 2, ... into the output in float32: the same order as
+    # reduce.cpp:44-62, so the results are bit-identical.
+    rng = np.random.default_rng(outer * 1000 + dim + inner)
+    x = rng.normal(size=(outer, dim, inner)).astype(np.float32)
+    z = orc.reduce_axis("sum", x, outer, dim, inner)
+    ref = np.add.reduce(x, axis=1, dtype=np.float32).ravel()
+    assert np.array_equal(z, ref)
+
+
+@pytest.mark.parametrize("outer,dim,inner", [(5, 9, 1), (3, 1024, 1), (2, 3, 7), (1, 1000, 1)])
+def test_sum_axis_integers_exact(orc, outer, dim, inner):
+    rng = np.random.default_rng(7 + outer + dim + inner)
+    x = rng.integers(-50, 51, size=(outer, dim, inner)).astype(np.float32)
+    z = orc.reduce_axis("sum", x, outer, dim, inner)
+    ref = x.astype(np.int64).sum(axis=1).ravel().astype(np.float32)
+    assert np.array_equal(z, ref)
+
+
+def test_sum_axis_row_equals_flat_per_row(orc):
+    # reduce.cpp:31-36: inner==1 runs the flat sum on every row.
+    x = KAT["sum_flat"][0]["x"]
+    rows = np.array([x, x[::-1]], np.float32)
+    z = orc.reduce_axis("sum", rows, 2, 8, 1)
+    assert z[0] == 6.0 and z[1] == orc.reduce_flat("sum", rows[1])[0]
+
+
+# ----------------------------------------------------------------- mean
+
+def test_mean_axis_reciprocal_body_division_tail(orc):
+    # 9 outputs, each a row [1,2,2] summing to 5.  reduce.cpp:77-80 multiplies
+    # the first 8 by rn(1/3) = 0x3eaaaaab: 5 * 0.333333343 = 1.66666672 rounds
+    # to 0x3fd55556; reduce.cpp:81-83 divides the 9th: rn(5/3) = 0x3fd55555.
+    case = KAT["mean_axis"][0]
+    x = np.tile(f32(case["row"]), case["outer"])
+    z = orc.reduce_axis("mean", x, case["outer"], case["dim"], case["inner"])
+    assert all(hexf(v) == case["expect_body_hex"] for v in z[:8])
+    assert hexf(z[8]) == case["expect_tail_hex"]
+
+
+@pytest.mark.parametrize("n", [1, 3, 8, 4096, 1 << 16])
+def test_mean_flat_is_sum_over_n(orc, n):
+    rng = np.random.default_rng(n)
+    x = rng.integers(-100, 101, size=n).astype(np.float32)
+    z = orc.reduce_flat("mean", x)[0]
+    s = int(x.astype(np.int64).sum())
+    assert z == np.float32(np.float32(s) / np.float32(n))
+
+
+# ------------------------------------------------------------ max / argmax
+
+@pytest.mark.parametrize("outer,dim,inner", [(1, 1, 1), (1, 13, 1), (7, 100, 1), (1, 9, 5), (4, 33, 17), (2, 8, 8)])
+def test_max_argmax_brute_force(orc, outer, dim, inner):
+    rng = np.random.default_rng(outer + 10 * dim + 100 * inner)
+    # quantised values so that ties are frequent; no -0.0 and no NaN
+    x = (rng.integers(-20, 21, size=(outer, dim, inner)) * 0.25).astype(np.float32)
+    zmax = orc.reduce_axis("max", x, outer, dim, inner)
+    zarg = orc.reduce_axis("argmax", x, outer, dim, inner)
+    assert np.array_equal(zmax, x.max(axis=1).ravel())
+    assert np.array_equal(zarg, x.argmax(axis=1).ravel().astype(np.int32))  # first occurrence
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 31, 1000])
+def test_max_argmax_flat_brute_force(orc, n):
+    rng = np.random.default_rng(1000 + n)
+    x = (rng.integers(-5, 6, size=n) * 0.5).astype(np.float32)
+    assert orc.reduce_flat("max", x)[0] == x.max()
+    assert orc.reduce_flat("argmax", x)[0] == int(np.argmax(x))
+
+
+def test_max_kats(orc):
+    c0, c1 = KAT["max"]
+    z = orc.reduce_flat("max", f32([float(v) for v in c0["x"]]))
+    assert hexf(z[0]) == c0["expect_hex"]  # -FLT_MAX, reduce.cpp:206
+    z = orc.reduce_axis("max", f32([float(v) for v in c1["x"]]), c1["outer"], c1["dim"], c1["inner"])
+    assert np.all(np.isneginf(z))
+
+
+@pytest.mark.parametrize("case", KAT["argmax"], ids=lambda c: c["name"])
+def test_argmax_kats(orc, case):
+    assert orc.reduce_flat("argmax", f32(case["x"]))[0] == case["expect"]
+
+
+# --------------------------------------------------- elementwise ops
+
+@pytest.mark.parametrize("op,npf", [(0, np.add), (1, np.subtract), (2, np.multiply), (3, np.divide)])
+def test_binary_bcast_scalar_vs_numpy_float32(orc, op, npf):
+    # numpy float32 arithmetic is IEEE single-rounded: the reference's
+    # _mm256_{add,sub,mul,div}_ps and scalar tails round the same way.
+    rng = np.random.default_rng(op)
+    x = rng.normal(size=(13, 29)).astype(np.float32)
+    y = rng.uniform(0.5, 2.0, size=(13, 29)).astype(np.float32)
+    r = rng.uniform(0.5, 2.0, size=29).astype(np.float32)
+    c = rng.uniform(0.5, 2.0, size=13).astype(np.float32)
+    assert np.array_equal(orc.binary(x, y, op), npf(x, y))
+    assert np.array_equal(orc.bcast_row(x, r, op), npf(x, r[None, :]))
+    assert np.array_equal(orc.bcast_col(x, c, op), npf(x, c[:, None]))
+    assert np.array_equal(orc.scalar(x, 0.37, op), npf(x, np.float32(0.37)))
+
+
+def test_binary_max_min(orc):
+    rng = np.random.default_rng(3)
+    x = rng.normal(size=1000).astype(np.float32)
+    y = rng.normal(size=1000).astype(np.float32)
+    assert np.array_equal(orc.binary(x, y, 4), np.maximum(x, y))
+    assert np.array_equal(orc.binary(x, y, 5), np.minimum(x, y))
+
+
+def test_relu_special_values(orc):
+    # max(0, x) = (0 > x) ? 0 : x: -0.0 and NaN pass through (functions.hpp:372-374)
+    x = f32([-0.0, np.nan, -1.0, 2.5, 0.0, -np.inf, np.inf])
+    z = orc.unary(x, 1)
+    assert np.signbit(z[0]) and z[0] == 0
+    assert np.isnan(z[1])
+    assert z[2] == 0 and not np.signbit(z[2])
+    assert z[3] == 2.5 and z[4] == 0 and z[5] == 0 and z[6] == np.inf
+    rng = np.random.default_rng(5)
+    v = rng.normal(size=10000).astype(np.float32)
+    assert np.array_equal(orc.unary(v, 1), np.maximum(v, np.float32(0)))
+
+
+@pytest.mark.parametrize("act,ref", [(2, lambda d: 1.0 / (1.0 + np.exp(-d))), (3, np.tanh), (4, np.exp)])
+def test_transcendentals_within_2ulp_of_float64(orc, act, ref):
+    rng = np.random.default_rng(act)
+    x = np.concatenate([rng.normal(0, 4, 200000), np.linspace(-20, 20, 100001)]).astype(np.float32)
+    if act == 4:
+        x = x[x < 80]
+    z = orc.unary(x, act)
+    with np.errstate(over="ignore"):
+        exact = ref(x.astype(np.float64)).astype(np.float32)
+    assert ulp_dist(z, exact).max() <= 2
+
+
+# -------------------------------------------------------------- softmax
+
+@pytest.mark.parametrize("name", ["sm_small", "sm_mask"])
+@pytest.mark.parametrize("mode", ["soft", "log"])
+def test_softmax_vs_torch_float64(orc, name, mode):
+    x = FIX[f"{name}_x"]
+    dy = FIX[f"{name}_dy"]
+    log = mode == "log"
+    y = orc.softmax_fwd(x, log)
+    ref = FIX[f"{name}_{mode}_y"]
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(y), fin)
+    if log:
+        assert np.all(np.isneginf(y[~fin]))
+        assert np.allclose(y[fin], ref[fin], rtol=1e-5, atol=1e-5)
+    else:
+        assert np.allclose(y, ref, rtol=1e-5, atol=1e-7)
+    dx = orc.softmax_bwd(y, dy, log)
+    refdx = FIX[f"{name}_{mode}_dx"]
+    scale = np.abs(refdx).max()
+    assert np.allclose(dx, refdx, rtol=1e-4, atol=1e-5 * scale)
+
+
+def test_softmax_invariants(orc):
+    rng = np.random.default_rng(11)
+    x = (rng.normal(size=(6, 1000)) * 8).astype(np.float32)
+    x[0] = 3.25  # constant row -> exactly 1/N after exp(0)=1, sum=N (exact), 1/N
+    x[1, ::3] = -np.inf
+    y = orc.softmax_fwd(x)
+    assert np.all(y[0] == np.float32(1.0) / np.float32(1000))
+    assert np.all(y[1, ::3] == 0)
+    assert np.allclose(y.astype(np.float64).sum(axis=1), 1.0, atol=1e-5)
+    yl = orc.softmax_fwd(x, log=True)
+    assert np.all(np.isneginf(yl[1, ::3]))
+    # shift invariance: adding a power of two that keeps x exact
+    y2 = orc.softmax_fwd(x + np.float32(64.0))
+    assert np.allclose(y2, y, rtol=1e-5, atol=1e-7)
+
+
+def test_affine_act_vs_torch_float64(orc):
+    x, s, b, dy = FIX["aff_x"], FIX["aff_scale"], FIX["aff_bias"], FIX["aff_dy"]
+    for act, an in ((1, "relu"), (2, "sigmoid"), (3, "tanh")):
+        y = orc.affine_act_fwd(x, s, b, act)
+        assert np.allclose(y, FIX[f"aff_{an}_y"], rtol=3e-7, atol=1e-7), an
+        dx, ds, db = orc.affine_act_bwd(x, s, y, dy, act)
+        assert np.allclose(dx, FIX[f"aff_{an}_dx"], rtol=1e-5, atol=1e-6), an
+        assert np.allclose(ds, FIX[f"aff_{an}_dscale"], rtol=1e-5, atol=1e-5), an
+        assert np.allclose(db, FIX[f"aff_{an}_dbias"], rtol=1e-5, atol=1e-5), an
+
+
+def test_affine_relu_forward_bit_exact_two_roundings(orc):
+    # forward relu is pure IEEE mul, add, select: numpy float32 gives the same bits
+    rng = np.random.default_rng(9)
+    x = rng.normal(size=(7, 45)).astype(np.float32)
+    s = rng.uniform(0.5, 1.5, 45).astype(np.float32)
+    b = rng.normal(0, 0.1, 45).astype(np.float32)
+    y = orc.affine_act_fwd(x, s, b, 1)
+    assert np.array_equal(y, np.maximum((x * s) + b, np.float32(0)))
+
+
+# --------------------------------------------------------------- matmul
+
+def test_matmul_k_panel_kat(orc):
+    # K=264, A = ones, B[:,0] = [2^24] + [1]*263.  Panel 0 (k<256): fma chain
+    # 2^24 + 1 + ... stays 2^24 (each +1 ties to even).  Panel 1: 8 ones = 8.
+    # C = 2^24 + 8 = 16777224 exactly.  One long chain would give 2^24; a
+    # 128-wide panel would give 2^24 + 136.
+    k = KAT["matmul"][0]["k"]
+    a = np.ones((1, k), np.float32)
+    b = np.ones((k, 3), np.float32)
+    b[0, 0] = 2.0 ** 24
+    c = orc.matmul(a, b)
+    assert c[0, 0] == np.float32(KAT["matmul"][0]["expect"])
+    assert c[0, 1] == k
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (9, 17, 13), (33, 300, 65), (64, 784, 10)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True)])
+def test_gemm_vs_float64(orc, m, k, n, ta, tb):
+    rng = np.random.default_rng(m * k + n)
+    a = rng.normal(size=(k, m) if ta else (m, k)).astype(np.float32)
+    b = rng.normal(size=(n, k) if tb else (k, n)).astype(np.float32)
+    c = orc.gemm(a, b, ta, tb)
+    A = (a.T if ta else a).astype(np.float64)
+    B = (b.T if tb else b).astype(np.float64)
+    ref = A @ B
+    bound = 1e-5 * (np.abs(A) @ np.abs(B))
+    assert np.all(np.abs(c - ref) <= bound)
+
+
+def test_matmul_small_integers_exact(orc):
+    rng = np.random.default_rng(2)
+    a = rng.integers(-8, 9, size=(20, 600)).astype(np.float32)
+    b = rng.integers(-8, 9, size=(600, 30)).astype(np.float32)
+    assert np.array_equal(orc.matmul(a, b), (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32))
+
+
+# ------------------------------------------------------------------ MLP
+
+def test_softmax_xent_vs_torch(orc):
+    loss, dl = orc.softmax_xent(FIX["xent_logits"], FIX["xent_labels"])
+    assert math.isclose(loss, float(FIX["xent_loss"][0]), rel_tol=1e-6)
+    assert np.allclose(dl, FIX["xent_dlogits"], rtol=1e-5, atol=1e-7)
+
+
+def test_sgd_two_roundings(orc):
+    w = f32([1.0, -2.0, 3.0])
+    g = f32([0.5, 0.25, -1.0])
+    assert np.array_equal(orc.sgd(w, g, 0.01), w - g * np.float32(0.01))
+
+
+def test_mlp_two_steps_vs_torch(orc):
+    x, lab = FIX["mlp_x"], FIX["mlp_labels"]
+    params = {k: FIX[f"mlp_init_{k}"].astype(np.float32).copy() for k in ("w1", "b1", "w2", "b2", "w3", "b3")}
+    losses = [orc.mlp_step(x, lab, params, 0.01) for _ in range(2)]
+    assert np.allclose(losses, FIX["mlp_losses"], rtol=1e-5)
+    for k, v in params.items():
+        ref = FIX[f"mlp_final_{k}"]
+        assert np.allclose(v, ref, rtol=1e-4, atol=1e-6), k
