@@ -1,0 +1,215 @@
+// Shared device helpers and host plumbing of the gfx950 kernels.
+//
+// Wave64 throughout: a wavefront is 64 lanes, a workgroup of 256 threads is
+// four waves.  Cross-lane reductions use DPP inside a row of 16 lanes
+// (quad_perm, row_half_mirror, row_mirror) and readlane across the four rows.
+// No float atomics anywhere: cross-workgroup combines are done in a fixed
+// order by the last workgroup to finish (an integer ticket per output), so
+// every result is deterministic run to run.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/cxm_hip.h"
+
+namespace cxm {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;  // threads per workgroup used by most kernels
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+// ------------------------------------------------------------ host side
+
+// Returns CXM_OK, or the HIP error of the last launch.
+int launch_status();
+
+// Scratch memory of the multi-pass kernels, one region per (device, stream).
+// The first `counter_words` 32-bit words are tickets, zero on entry to every
+// kernel (each kernel's last workgroup puts its tickets back to zero); the
+// rest is partial results.  Grows on demand (after a stream sync).
+struct Workspace {
+    unsigned *counters;
+    size_t counter_words;
+    void *scratch;
+    size_t scratch_bytes;
+};
+int get_workspace(cxm_stream_t s, size_t counter_words, size_t scratch_bytes, Workspace *ws);
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline unsigned ceil_div(size_t a, size_t b) { return static_cast<unsigned>((a + b - 1) / b); }
+
+// ---------------------------------------------------------- device side
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+
+// DPP controls (all sources in range, so every lane is written).
+constexpr int kQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+__device__ __forceinline__ int readlane(int v, int lane) {
+    return __builtin_amdgcn_readlane(v, lane);
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 128-bit loads/stores.  The streaming forms set the non-temporal hint for
+// data touched once (inputs of a reduction, outputs of an elementwise op).
+__device__ __forceinline__ float4 ld4(const float *p) {
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 ld4_stream(const float *p) {
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st4(float *p, float4 v) {
+    *reinterpret_cast<f32x4 *>(p) = f32x4{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ void st4_stream(float *p, float4 v) {
+    __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4 *>(p));
+}
+
+// IEEE max as _mm256_max_ps(a, b): a when a > b, else b.
+__device__ __forceinline__ float vmax(float a, float b) { return a > b ? a : b; }
+
+// Reduction operators.  `combine` must be associative and commutative on the
+// values the kernels feed it (sum: up to rounding; max/argmax: exactly, for
+// non-NaN inputs).
+struct SumOp {
+    using T = float;
+    __device__ static T identity() { return 0.0f; }
+    __device__ static T combine(T a, T b) { return a + b; }
+    __device__ static T from(float v, int) { return v; }
+};
+
+struct MaxOp {
+    using T = float;
+    __device__ static T identity() { return -FLT_MAX; }
+    __device__ static T combine(T a, T b) { return vmax(a, b); }
+    __device__ static T from(float v, int) { return v; }
+};
+
+// Lexicographic (value, index): larger value wins; equal values keep the
+// smaller index, i.e. the first maximum in storage order.
+struct ArgPair {
+    float v;
+    int i;
+};
+struct ArgMaxOp {
+    using T = ArgPair;
+    __device__ static T identity() { return {-INFINITY, 0x7fffffff}; }
+    __device__ static T combine(T a, T b) {
+        const bool take_b = (b.v > a.v) || (b.v == a.v && b.i < a.i);
+        return take_b ? b : a;
+    }
+    __device__ static T from(float v, int i) { return {v, i}; }
+};
+
+template <int CTRL>
+__device__ __forceinline__ ArgPair dpp(ArgPair p) {
+    return {dpp<CTRL>(p.v), dpp<CTRL>(p.i)};
+}
+__device__ __forceinline__ ArgPair readlane(ArgPair p, int lane) {
+    return {readlane(p.v, lane), readlane(p.i, lane)};
+}
+
+// Reduce across the 64 lanes of a wave; every lane gets the result.
+// Must be called with all 64 lanes active.
+template <class Op>
+__device__ __forceinline__ typename Op::T wave_reduce(typename Op::T v) {
+    v = Op::combine(v, dpp<kQuadXor1>(v));
+    v = Op::combine(v, dpp<kQuadXor2>(v));
+    v = Op::combine(v, dpp<kRowHalfMirror>(v));
+    v = Op::combine(v, dpp<kRowMirror>(v));
+    typename Op::T r = Op::combine(Op::combine(readlane(v, 0), readlane(v, 16)),
+                                   Op::combine(readlane(v, 32), readlane(v, 48)));
+    return r;
+}
+
+// Reduce across a workgroup of NT threads; the result is valid in every
+// thread.  `lds` must hold NT/64 elements.  Contains barriers: call from
+// uniform control flow.
+template <class Op, int NT>
+__device__ __forceinline__ typename Op::T block_reduce(typename Op::T v, typename Op::T *lds) {
+    constexpr int NW = NT / kWave;
+    v = wave_reduce<Op>(v);
+    if constexpr (NW == 1) {
+        return v;
+    } else {
+        const int w = threadIdx.x / kWave;
+        if ((threadIdx.x & (kWave - 1)) == 0) lds[w] = v;
+        __syncthreads();
+        typename Op::T r = lds[0];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) r = Op::combine(r, lds[i]);
+        __syncthreads();  // lds may be reused by the caller
+        return r;
+    }
+}
+
+// Device-coherent stores and loads for data that one workgroup hands to
+// another within a kernel (partial results).  They are agent-scope relaxed
+// atomics: the store is written through past this XCD's L2 (sc1) and the
+// load does not trust the reader's L2, so no L2 write-back or invalidate of
+// the whole cache is needed (a __threadfence() per workgroup costs that on
+// a multi-XCD part, and dominated the run time of a 2048-workgroup grid).
+__device__ __forceinline__ void st_dev(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(ArgPair *p, ArgPair v) {
+    const unsigned long long u = (static_cast<unsigned long long>(static_cast<unsigned>(v.i)) << 32) |
+                                 __builtin_bit_cast(unsigned, v.v);
+    __hip_atomic_store(reinterpret_cast<unsigned long long *>(p), u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ ArgPair ld_dev(const ArgPair *p) {
+    const unsigned long long u = __hip_atomic_load(reinterpret_cast<const unsigned long long *>(p),
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return {__builtin_bit_cast(float, static_cast<unsigned>(u)), static_cast<int>(u >> 32)};
+}
+
+// Last-workgroup ticket.  Every thread of the workgroup calls it after
+// storing its share of the workgroup's partials with st_dev; returns true in
+// all threads of the one workgroup that arrives last among `expected`, which
+// then reads every partial with ld_dev.  Ordering: each thread waits for its
+// own stores to complete (vmcnt 0) before the barrier, and the ticket is an
+// agent-scope atomic issued after the barrier, so every partial is at the
+// coherent level before the count can reach `expected`.
+__device__ __forceinline__ bool last_block_ticket(unsigned *counter, unsigned expected,
+                                                  int *lds_flag) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned t =
+            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = (t == expected - 1);
+        // ready for the next kernel that uses this workspace
+        if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *lds_flag = last ? 1 : 0;
+    }
+    __syncthreads();
+    return *lds_flag != 0;
+}
+
+}  // namespace cxm

@@ -1,0 +1,616 @@
+// Elementwise fp32 kernels: same-shape binary ops, row/column broadcast,
+// tensor-op-scalar, unary activations, the fused affine + activation
+// forward/backward of the C3 workload, and the SGD update.
+//
+// Replaces the float4 grid-stride loops of the reference's CUDA path
+// (kernels::Binary / kernels::scalar / kernels::Unary,
+// source/CortexMind/framework/Engine/Kernels/binary.cuh:15-39,
+// scalar.cuh:30-54, unary.cuh:16-40) and the CPU Broadcast::row/col
+// (Engine/AVX2/broadcast.cpp:182-388), which has no GPU form there.
+//
+// Every op rounds exactly as the reference's scalar expression does: the
+// library is built with -ffp-contract=off, so x*s+b is a rounded product
+// followed by a rounded sum, never an fma.  ReLU is an explicit select
+// (0 > t ? 0 : t), matching _mm256_max_ps(0, t) for -0.0 and NaN.
+#include "cxm_common.hpp"
+
+namespace cxm {
+namespace {
+
+__device__ __forceinline__ float bin(int op, float a, float b) {
+    switch (op) {
+        case CXM_OP_ADD: return a + b;
+        case CXM_OP_SUB: return a - b;
+        case CXM_OP_MUL: return a * b;
+        case CXM_OP_DIV: return a / b;
+        case CXM_OP_MAX: return a > b ? a : b;
+        default: return a < b ? a : b;
+    }
+}
+
+template <int OP>
+__device__ __forceinline__ float bin_t(float a, float b) {
+    if constexpr (OP == CXM_OP_ADD) return a + b;
+    else if constexpr (OP == CXM_OP_SUB) return a - b;
+    else if constexpr (OP == CXM_OP_MUL) return a * b;
+    else if constexpr (OP == CXM_OP_DIV) return a / b;
+    else if constexpr (OP == CXM_OP_MAX) return a > b ? a : b;
+    else return a < b ? a : b;
+}
+
+template <int OP>
+__device__ __forceinline__ float4 bin4(float4 a, float4 b) {
+    return make_float4(bin_t<OP>(a.x, b.x), bin_t<OP>(a.y, b.y), bin_t<OP>(a.z, b.z),
+                       bin_t<OP>(a.w, b.w));
+}
+
+// relu: functions.hpp:372-374; sigmoid: functions.hpp:405-411 (1/(1+exp(-x)));
+// tanh: functions.hpp:381-383; exp: functions.hpp:186-188.
+template <int ACT>
+__device__ __forceinline__ float act(float t) {
+    if constexpr (ACT == CXM_ACT_RELU) return 0.0f > t ? 0.0f : t;
+    else if constexpr (ACT == CXM_ACT_SIGMOID) {
+        const float e = expf(-t);
+        const float d = 1.0f + e;
+        return 1.0f / d;
+    } else if constexpr (ACT == CXM_ACT_TANH) return tanhf(t);
+    else if constexpr (ACT == CXM_ACT_EXP) return expf(t);
+    else return t;
+}
+
+template <int ACT>
+__device__ __forceinline__ float4 act4(float4 t) {
+    return make_float4(act<ACT>(t.x), act<ACT>(t.y), act<ACT>(t.z), act<ACT>(t.w));
+}
+
+// Derivative factor from the saved output y (one rounding per operation):
+// relu' = y > 0, sigmoid' = y*(1-y), tanh' = 1 - y*y.
+template <int ACT>
+__device__ __forceinline__ float dact(float y) {
+    if constexpr (ACT == CXM_ACT_RELU) return y > 0.0f ? 1.0f : 0.0f;
+    else if constexpr (ACT == CXM_ACT_SIGMOID) {
+        const float t = 1.0f - y;
+        return y * t;
+    } else if constexpr (ACT == CXM_ACT_TANH) {
+        const float t = y * y;
+        return 1.0f - t;
+    } else return 1.0f;
+}
+
+// Grid for a flat streaming kernel: enough workgroups to fill 256 CUs
+// several times over, each thread then strides through the rest.
+inline unsigned stream_grid(size_t n4) {
+    size_t b = (n4 + kBlock - 1) / kBlock;
+    const size_t cap = 256 * 16;
+    return static_cast<unsigned>(b < 1 ? 1 : (b > cap ? cap : b));
+}
+
+// -------------------------------------------------------------- binary
+
+template <int OP>
+__global__ __launch_bounds__(kBlock) void k_binary_vec(const float *__restrict__ x,
+                                                       const float *__restrict__ y, float *z,
+                                                       size_t n) {
+    const size_t n4 = n / 4;
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride)
+        st4(z + 4 * i, bin4<OP>(ld4(x + 4 * i), ld4(y + 4 * i)));
+    // tail (n % 4 elements) by the first threads of block 0
+    if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
+        const size_t j = 4 * n4 + threadIdx.x;
+        z[j] = bin_t<OP>(x[j], y[j]);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void k_binary_scalar(const float *x, const float *y, float *z,
+                                                          size_t n, int op) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+        z[i] = bin(op, x[i], y[i]);
+}
+
+// ------------------------------------------------------------ broadcast
+
+// Row broadcast z[i,j] = x[i,j] op y[j], n % 4 == 0: a thread keeps one
+// float4 of y and walks rows.  grid.x = column tiles of 256 float4, grid.y
+// = row chunks.
+template <int OP>
+__global__ __launch_bounds__(kBlock) void k_bcast_row_vec(const float *x, const float *__restrict__ y,
+                                                          float *z, size_t m, size_t n,
+                                                          size_t rows_per_chunk) {
+    const size_t j4 = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (4 * j4 >= n) return;
+    const float4 yv = ld4(y + 4 * j4);
+    const size_t r0 = static_cast<size_t>(blockIdx.y) * rows_per_chunk;
+    const size_t r1 = r0 + rows_per_chunk < m ? r0 + rows_per_chunk : m;
+    for (size_t r = r0; r < r1; ++r) {
+        const size_t o = r * n + 4 * j4;
+        st4(z + o, bin4<OP>(ld4(x + o), yv));
+    }
+}
+
+// Column broadcast z[i,j] = x[i,j] op y[i], n % 4 == 0.
+template <int OP>
+__global__ __launch_bounds__(kBlock) void k_bcast_col_vec(const float *x, const float *__restrict__ y,
+                                                          float *z, size_t m, size_t n,
+                                                          size_t rows_per_chunk) {
+    const size_t j4 = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (4 * j4 >= n) return;
+    const size_t r0 = static_cast<size_t>(blockIdx.y) * rows_per_chunk;
+    const size_t r1 = r0 + rows_per_chunk < m ? r0 + rows_per_chunk : m;
+    for (size_t r = r0; r < r1; ++r) {
+        const float v = y[r];
+        const size_t o = r * n + 4 * j4;
+        st4(z + o, bin4<OP>(ld4(x + o), make_float4(v, v, v, v)));
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void k_bcast_scalar(const float *x, const float *y, float *z,
+                                                         size_t m, size_t n, int op, int row_mode) {
+    const size_t total = m * n;
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride) {
+        const size_t r = i / n;
+        const size_t c = i - r * n;
+        z[i] = bin(op, x[i], row_mode ? y[c] : y[r]);
+    }
+}
+
+// --------------------------------------------------------------- scalar
+
+template <int OP>
+__global__ __launch_bounds__(kBlock) void k_scalar_vec(const float *x, float v, float *z, size_t n) {
+    const size_t n4 = n / 4;
+    const float4 vv = make_float4(v, v, v, v);
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride)
+        st4(z + 4 * i, bin4<OP>(ld4(x + 4 * i), vv));
+    if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
+        const size_t j = 4 * n4 + threadIdx.x;
+        z[j] = bin_t<OP>(x[j], v);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void k_scalar_scalar(const float *x, float v, float *z, size_t n,
+                                                          int op) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+        z[i] = bin(op, x[i], v);
+}
+
+// ---------------------------------------------------------------- unary
+
+template <int ACT, bool VEC>
+__global__ __launch_bounds__(kBlock) void k_unary(const float *x, float *z, size_t n) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if constexpr (VEC) {
+        const size_t n4 = n / 4;
+        for (; i < n4; i += stride) st4(z + 4 * i, act4<ACT>(ld4(x + 4 * i)));
+        if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
+            const size_t j = 4 * n4 + threadIdx.x;
+            z[j] = act<ACT>(x[j]);
+        }
+    } else {
+        for (; i < n; i += stride) z[i] = act<ACT>(x[i]);
+    }
+}
+
+// ------------------------------------------------------ affine forward
+
+// y = act(x*scale[j] + bias[j]) over [m, n], n % 4 == 0.  A thread owns one
+// float4 of columns (scale and bias loaded once) and UNR rows at a time.
+template <int ACT, int UNR>
+__global__ __launch_bounds__(kBlock) void k_affine_fwd_vec(const float *__restrict__ x,
+                                                           const float *__restrict__ scale,
+                                                           const float *__restrict__ bias,
+                                                           float *__restrict__ y, size_t m, size_t n,
+                                                           size_t rows_per_chunk) {
+    const size_t j4 = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (4 * j4 >= n) return;
+    const float4 s = ld4(scale + 4 * j4);
+    const float4 b = ld4(bias + 4 * j4);
+    const size_t r0 = static_cast<size_t>(blockIdx.y) * rows_per_chunk;
+    const size_t r1 = r0 + rows_per_chunk < m ? r0 + rows_per_chunk : m;
+    size_t r = r0;
+    for (; r + UNR <= r1; r += UNR) {
+        float4 v[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) v[u] = ld4_stream(x + (r + u) * n + 4 * j4);
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            float4 t;
+            t.x = v[u].x * s.x; t.y = v[u].y * s.y; t.z = v[u].z * s.z; t.w = v[u].w * s.w;
+            t.x = t.x + b.x; t.y = t.y + b.y; t.z = t.z + b.z; t.w = t.w + b.w;
+            st4_stream(y + (r + u) * n + 4 * j4, act4<ACT>(t));
+        }
+    }
+    for (; r < r1; ++r) {
+        const float4 v = ld4_stream(x + r * n + 4 * j4);
+        float4 t;
+        t.x = v.x * s.x; t.y = v.y * s.y; t.z = v.z * s.z; t.w = v.w * s.w;
+        t.x = t.x + b.x; t.y = t.y + b.y; t.z = t.z + b.z; t.w = t.w + b.w;
+        st4_stream(y + r * n + 4 * j4, act4<ACT>(t));
+    }
+}
+
+template <int ACT>
+__global__ __launch_bounds__(kBlock) void k_affine_fwd_scalar(const float *x, const float *scale,
+                                                              const float *bias, float *y, size_t m,
+                                                              size_t n) {
+    const size_t total = m * n;
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride) {
+        const size_t c = i % n;
+        float t = x[i] * scale[c];
+        t = t + bias[c];
+        y[i] = act<ACT>(t);
+    }
+}
+
+// ----------------------------------------------------- affine backward
+
+// dz = dy*act'(y); dx = dz*scale[j]; dscale[j] = sum_i dz*x; dbias[j] = sum_i dz.
+// Workgroup = 256 columns (64 lanes x float4) x a chunk of rows; the four
+// waves take interleaved rows and meet in LDS; chunks are combined in
+// chunk order by the last workgroup of the column tile.
+constexpr int kAffTile = 256;
+
+template <int ACT, bool VEC, int UNR>
+__global__ __launch_bounds__(kBlock) void k_affine_bwd(const float *__restrict__ x,
+                                                       const float *__restrict__ scale,
+                                                       const float *__restrict__ y,
+                                                       const float *__restrict__ dy,
+                                                       float *__restrict__ dx,
+                                                       float *__restrict__ dscale,
+                                                       float *__restrict__ dbias, size_t m, size_t n,
+                                                       unsigned ntiles, unsigned chunks,
+                                                       size_t rows_per_chunk,
+                                                       float *__restrict__ part,
+                                                       unsigned *__restrict__ counters) {
+    __shared__ float lds_s[kWavesPerBlock][kAffTile];
+    __shared__ float lds_b[kWavesPerBlock][kAffTile];
+    __shared__ int flag;
+    const unsigned tile = blockIdx.x % ntiles;
+    const unsigned chunk = blockIdx.x / ntiles;
+    const int tid = threadIdx.x;
+    const size_t r0 = static_cast<size_t>(chunk) * rows_per_chunk;
+    const size_t r1 = r0 + rows_per_chunk < m ? r0 + rows_per_chunk : m;
+    float ms, mb;  // this thread's column (tile*256 + tid) over the chunk
+
+    if constexpr (VEC) {
+        const int lane = tid & (kWave - 1);
+        const int w = tid / kWave;
+        const size_t col = static_cast<size_t>(tile) * kAffTile + lane * 4;
+        float as[4] = {0, 0, 0, 0}, ab[4] = {0, 0, 0, 0};
+        if (col < n) {
+            const float4 sc = ld4(scale + col);
+            size_t r = r0 + w;
+            auto body = [&](size_t rr, float4 xv, float4 yv, float4 gv) {
+                float4 dz;
+                dz.x = gv.x * dact<ACT>(yv.x); dz.y = gv.y * dact<ACT>(yv.y);
+                dz.z = gv.z * dact<ACT>(yv.z); dz.w = gv.w * dact<ACT>(yv.w);
+                float4 d;
+                d.x = dz.x * sc.x; d.y = dz.y * sc.y; d.z = dz.z * sc.z; d.w = dz.w * sc.w;
+                st4_stream(dx + rr * n + col, d);
+                const float p0 = dz.x * xv.x, p1 = dz.y * xv.y, p2 = dz.z * xv.z, p3 = dz.w * xv.w;
+                as[0] = as[0] + p0; as[1] = as[1] + p1; as[2] = as[2] + p2; as[3] = as[3] + p3;
+                ab[0] = ab[0] + dz.x; ab[1] = ab[1] + dz.y; ab[2] = ab[2] + dz.z; ab[3] = ab[3] + dz.w;
+            };
+            for (; r + (UNR - 1) * kWavesPerBlock < r1; r += UNR * kWavesPerBlock) {
+                float4 xv[UNR], yv[UNR], gv[UNR];
+#pragma unroll
+                for (int u = 0; u < UNR; ++u) {
+                    const size_t o = (r + u * kWavesPerBlock) * n + col;
+                    xv[u] = ld4_stream(x + o);
+                    yv[u] = ld4_stream(y + o);
+                    gv[u] = ld4_stream(dy + o);
+                }
+#pragma unroll
+                for (int u = 0; u < UNR; ++u) body(r + u * kWavesPerBlock, xv[u], yv[u], gv[u]);
+            }
+            for (; r < r1; r += kWavesPerBlock) {
+                const size_t o = r * n + col;
+                body(r, ld4_stream(x + o), ld4_stream(y + o), ld4_stream(dy + o));
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            lds_s[w][lane * 4 + c] = as[c];
+            lds_b[w][lane * 4 + c] = ab[c];
+        }
+        __syncthreads();
+        ms = (lds_s[0][tid] + lds_s[1][tid]) + (lds_s[2][tid] + lds_s[3][tid]);
+        mb = (lds_b[0][tid] + lds_b[1][tid]) + (lds_b[2][tid] + lds_b[3][tid]);
+    } else {
+        const size_t col = static_cast<size_t>(tile) * kAffTile + tid;
+        ms = 0.0f;
+        mb = 0.0f;
+        if (col < n) {
+            const float sc = scale[col];
+            for (size_t r = r0; r < r1; ++r) {
+                const size_t o = r * n + col;
+                const float dz = dy[o] * dact<ACT>(y[o]);
+                dx[o] = dz * sc;
+                const float p = dz * x[o];
+                ms = ms + p;
+                mb = mb + dz;
+            }
+        }
+    }
+
+    const size_t col = static_cast<size_t>(tile) * kAffTile + tid;
+    if (chunks == 1) {
+        if (col < n) {
+            dscale[col] = ms;
+            dbias[col] = mb;
+        }
+        return;
+    }
+    const size_t slot = static_cast<size_t>(tile) * chunks;
+    st_dev(&part[((slot + chunk) * 2 + 0) * kAffTile + tid], ms);
+    st_dev(&part[((slot + chunk) * 2 + 1) * kAffTile + tid], mb);
+    if (!last_block_ticket(&counters[tile], chunks, &flag)) return;
+    float a = 0.0f, bsum = 0.0f;
+    for (unsigned c = 0; c < chunks; ++c) {
+        a = a + ld_dev(&part[((slot + c) * 2 + 0) * kAffTile + tid]);
+        bsum = bsum + ld_dev(&part[((slot + c) * 2 + 1) * kAffTile + tid]);
+    }
+    if (col < n) {
+        dscale[col] = a;
+        dbias[col] = bsum;
+    }
+}
+
+// ------------------------------------------------------------------ sgd
+
+// w = w - g*lr, two roundings (matrix_t::sub of ScalarOp::mul).
+__global__ __launch_bounds__(kBlock) void k_sgd(float *w, const float *__restrict__ g, float lr,
+                                                size_t n, int vec) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (vec) {
+        const size_t n4 = n / 4;
+        for (; i < n4; i += stride) {
+            const float4 gv = ld4(g + 4 * i);
+            float4 wv = ld4(w + 4 * i);
+            float4 t;
+            t.x = gv.x * lr; t.y = gv.y * lr; t.z = gv.z * lr; t.w = gv.w * lr;
+            wv.x = wv.x - t.x; wv.y = wv.y - t.y; wv.z = wv.z - t.z; wv.w = wv.w - t.w;
+            st4(w + 4 * i, wv);
+        }
+        if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
+            const size_t j = 4 * n4 + threadIdx.x;
+            const float t = g[j] * lr;
+            w[j] = w[j] - t;
+        }
+    } else {
+        for (; i < n; i += stride) {
+            const float t = g[i] * lr;
+            w[i] = w[i] - t;
+        }
+    }
+}
+
+// ----------------------------------------------------------------- host
+
+inline hipStream_t hs(cxm_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+template <template <int> class L, class... A>
+int dispatch_op(int op, A... a) {
+    switch (op) {
+        case CXM_OP_ADD: return L<CXM_OP_ADD>::run(a...);
+        case CXM_OP_SUB: return L<CXM_OP_SUB>::run(a...);
+        case CXM_OP_MUL: return L<CXM_OP_MUL>::run(a...);
+        case CXM_OP_DIV: return L<CXM_OP_DIV>::run(a...);
+        case CXM_OP_MAX: return L<CXM_OP_MAX>::run(a...);
+        case CXM_OP_MIN: return L<CXM_OP_MIN>::run(a...);
+        default: return CXM_E_INVALID;
+    }
+}
+
+template <int OP>
+struct BinaryL {
+    static int run(const float *x, const float *y, float *z, size_t n, hipStream_t s) {
+        hipLaunchKernelGGL(k_binary_vec<OP>, dim3(stream_grid(n / 4)), dim3(kBlock), 0, s, x, y, z, n);
+        return launch_status();
+    }
+};
+
+template <int OP>
+struct ScalarL {
+    static int run(const float *x, float v, float *z, size_t n, hipStream_t s) {
+        hipLaunchKernelGGL(k_scalar_vec<OP>, dim3(stream_grid(n / 4)), dim3(kBlock), 0, s, x, v, z, n);
+        return launch_status();
+    }
+};
+
+// grid for the [m, n] column-tile x row-chunk kernels
+inline void tile_grid(size_t m, size_t n, dim3 *grid, size_t *rpc) {
+    const size_t tiles = (n / 4 + kBlock - 1) / kBlock;
+    size_t chunks = (4096 + tiles - 1) / tiles;
+    if (chunks > m) chunks = m;
+    if (chunks < 1) chunks = 1;
+    if (chunks > 65535) chunks = 65535;
+    *rpc = (m + chunks - 1) / chunks;
+    chunks = (m + *rpc - 1) / *rpc;
+    *grid = dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(chunks));
+}
+
+template <int OP>
+struct BcastL {
+    static int run(const float *x, const float *y, float *z, size_t m, size_t n, int row_mode,
+                   hipStream_t s) {
+        dim3 grid;
+        size_t rpc;
+        tile_grid(m, n, &grid, &rpc);
+        if (row_mode)
+            hipLaunchKernelGGL(k_bcast_row_vec<OP>, grid, dim3(kBlock), 0, s, x, y, z, m, n, rpc);
+        else
+            hipLaunchKernelGGL(k_bcast_col_vec<OP>, grid, dim3(kBlock), 0, s, x, y, z, m, n, rpc);
+        return launch_status();
+    }
+};
+
+int bcast(const float *x, const float *y, float *z, size_t m, size_t n, int op, int row_mode,
+          cxm_stream_t s) {
+    if (!x || !y || !z || op < CXM_OP_ADD || op > CXM_OP_DIV) return CXM_E_INVALID;
+    if (m == 0 || n == 0) return CXM_OK;
+    if (n % 4 == 0 && aligned16(x) && aligned16(z) && (!row_mode || aligned16(y)))
+        return dispatch_op<BcastL>(op, x, y, z, m, n, row_mode, hs(s));
+    hipLaunchKernelGGL(k_bcast_scalar, dim3(stream_grid((m * n + 3) / 4)), dim3(kBlock), 0, hs(s), x,
+                       y, z, m, n, op, row_mode);
+    return launch_status();
+}
+
+template <int ACT>
+int unary_t(const float *x, float *z, size_t n, hipStream_t s) {
+    if (aligned16(x) && aligned16(z))
+        hipLaunchKernelGGL((k_unary<ACT, true>), dim3(stream_grid(n / 4)), dim3(kBlock), 0, s, x, z, n);
+    else
+        hipLaunchKernelGGL((k_unary<ACT, false>), dim3(stream_grid((n + 3) / 4)), dim3(kBlock), 0, s, x,
+                           z, n);
+    return launch_status();
+}
+
+template <int ACT>
+int affine_fwd_t(const float *x, const float *scale, const float *bias, float *y, size_t m,
+                 size_t n, hipStream_t s) {
+    if (n % 4 == 0 && aligned16(x) && aligned16(scale) && aligned16(bias) && aligned16(y)) {
+        dim3 grid;
+        size_t rpc;
+        tile_grid(m, n, &grid, &rpc);
+        hipLaunchKernelGGL((k_affine_fwd_vec<ACT, 4>), grid, dim3(kBlock), 0, s, x, scale, bias, y, m,
+                           n, rpc);
+    } else {
+        hipLaunchKernelGGL(k_affine_fwd_scalar<ACT>, dim3(stream_grid((m * n + 3) / 4)), dim3(kBlock), 0,
+                           s, x, scale, bias, y, m, n);
+    }
+    return launch_status();
+}
+
+template <int ACT>
+int affine_bwd_t(const float *x, const float *scale, const float *y, const float *dy, float *dx,
+                 float *dscale, float *dbias, size_t m, size_t n, cxm_stream_t st) {
+    const bool vec = n % 4 == 0 && aligned16(x) && aligned16(scale) && aligned16(y) &&
+                     aligned16(dy) && aligned16(dx);
+    const size_t ntiles = (n + kAffTile - 1) / kAffTile;
+    size_t chunks = (2048 + ntiles - 1) / ntiles;
+    const size_t max_chunks = (m + 15) / 16;
+    if (chunks > max_chunks) chunks = max_chunks;
+    if (chunks < 1) chunks = 1;
+    size_t rpc = (m + chunks - 1) / chunks;
+    rpc = (rpc + 3) / 4 * 4;
+    chunks = (m + rpc - 1) / rpc;
+    if (chunks < 1) chunks = 1;
+    if (ntiles * chunks > 0x7fffffffu) return CXM_E_TOO_LARGE;
+    float *part = nullptr;
+    unsigned *counters = nullptr;
+    if (chunks > 1) {
+        Workspace ws;
+        int rc = get_workspace(st, ntiles, ntiles * chunks * 2 * kAffTile * sizeof(float), &ws);
+        if (rc) return rc;
+        part = static_cast<float *>(ws.scratch);
+        counters = ws.counters;
+    }
+    const dim3 grid(static_cast<unsigned>(ntiles * chunks));
+    if (vec)
+        hipLaunchKernelGGL((k_affine_bwd<ACT, true, 4>), grid, dim3(kBlock), 0, hs(st), x, scale, y,
+                           dy, dx, dscale, dbias, m, n, static_cast<unsigned>(ntiles),
+                           static_cast<unsigned>(chunks), rpc, part, counters);
+    else
+        hipLaunchKernelGGL((k_affine_bwd<ACT, false, 1>), grid, dim3(kBlock), 0, hs(st), x, scale, y,
+                           dy, dx, dscale, dbias, m, n, static_cast<unsigned>(ntiles),
+                           static_cast<unsigned>(chunks), rpc, part, counters);
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace cxm
+
+using namespace cxm;
+
+extern "C" {
+
+int cxm_binary_f32(const float *x, const float *y, float *z, size_t n, int op, cxm_stream_t s) {
+    if (!x || !y || !z || op < CXM_OP_ADD || op > CXM_OP_MIN) return CXM_E_INVALID;
+    if (n == 0) return CXM_OK;
+    if (aligned16(x) && aligned16(y) && aligned16(z)) return dispatch_op<BinaryL>(op, x, y, z, n, hs(s));
+    hipLaunchKernelGGL(k_binary_scalar, dim3(stream_grid((n + 3) / 4)), dim3(kBlock), 0, hs(s), x, y, z,
+                       n, op);
+    return launch_status();
+}
+
+int cxm_bcast_row_f32(const float *x, const float *y, float *z, size_t m, size_t n, int op,
+                      cxm_stream_t s) {
+    return bcast(x, y, z, m, n, op, 1, s);
+}
+
+int cxm_bcast_col_f32(const float *x, const float *y, float *z, size_t m, size_t n, int op,
+                      cxm_stream_t s) {
+    return bcast(x, y, z, m, n, op, 0, s);
+}
+
+int cxm_scalar_f32(const float *x, float value, float *z, size_t n, int op, cxm_stream_t s) {
+    if (!x || !z || op < CXM_OP_ADD || op > CXM_OP_MIN) return CXM_E_INVALID;
+    if (n == 0) return CXM_OK;
+    if (aligned16(x) && aligned16(z)) return dispatch_op<ScalarL>(op, x, value, z, n, hs(s));
+    hipLaunchKernelGGL(k_scalar_scalar, dim3(stream_grid((n + 3) / 4)), dim3(kBlock), 0, hs(s), x, value,
+                       z, n, op);
+    return launch_status();
+}
+
+int cxm_unary_f32(const float *x, float *z, size_t n, int act, cxm_stream_t s) {
+    if (!x || !z) return CXM_E_INVALID;
+    if (n == 0) return CXM_OK;
+    switch (act) {
+        case CXM_ACT_RELU: return unary_t<CXM_ACT_RELU>(x, z, n, hs(s));
+        case CXM_ACT_SIGMOID: return unary_t<CXM_ACT_SIGMOID>(x, z, n, hs(s));
+        case CXM_ACT_TANH: return unary_t<CXM_ACT_TANH>(x, z, n, hs(s));
+        case CXM_ACT_EXP: return unary_t<CXM_ACT_EXP>(x, z, n, hs(s));
+        default: return CXM_E_INVALID;
+    }
+}
+
+int cxm_affine_act_fwd_f32(const float *x, const float *scale, const float *bias, float *y,
+                           size_t m, size_t n, int act, cxm_stream_t s) {
+    if (!x || !scale || !bias || !y) return CXM_E_INVALID;
+    if (m == 0 || n == 0) return CXM_OK;
+    switch (act) {
+        case CXM_ACT_NONE: return affine_fwd_t<CXM_ACT_NONE>(x, scale, bias, y, m, n, hs(s));
+        case CXM_ACT_RELU: return affine_fwd_t<CXM_ACT_RELU>(x, scale, bias, y, m, n, hs(s));
+        case CXM_ACT_SIGMOID: return affine_fwd_t<CXM_ACT_SIGMOID>(x, scale, bias, y, m, n, hs(s));
+        case CXM_ACT_TANH: return affine_fwd_t<CXM_ACT_TANH>(x, scale, bias, y, m, n, hs(s));
+        default: return CXM_E_INVALID;
+    }
+}
+
+int cxm_affine_act_bwd_f32(const float *x, const float *scale, const float *y, const float *dy,
+                           float *dx, float *dscale, float *dbias, size_t m, size_t n, int act,
+                           cxm_stream_t s) {
+    if (!x || !scale || !y || !dy || !dx || !dscale || !dbias) return CXM_E_INVALID;
+    if (n == 0) return CXM_OK;
+    if (m == 0) return CXM_E_INVALID;  // column sums over zero rows are undefined in the reference
+    switch (act) {
+        case CXM_ACT_NONE:
+            return affine_bwd_t<CXM_ACT_NONE>(x, scale, y, dy, dx, dscale, dbias, m, n, s);
+        case CXM_ACT_RELU:
+            return affine_bwd_t<CXM_ACT_RELU>(x, scale, y, dy, dx, dscale, dbias, m, n, s);
+        case CXM_ACT_SIGMOID:
+            return affine_bwd_t<CXM_ACT_SIGMOID>(x, scale, y, dy, dx, dscale, dbias, m, n, s);
+        case CXM_ACT_TANH:
+            return affine_bwd_t<CXM_ACT_TANH>(x, scale, y, dy, dx, dscale, dbias, m, n, s);
+        default: return CXM_E_INVALID;
+    }
+}
+
+int cxm_sgd_f32(float *w, const float *g, float lr, size_t n, cxm_stream_t s) {
+    if (!w || !g) return CXM_E_INVALID;
+    if (n == 0) return CXM_OK;
+    const int vec = aligned16(w) && aligned16(g);
+    hipLaunchKernelGGL(k_sgd, dim3(stream_grid(vec ? n / 4 : (n + 3) / 4)), dim3(kBlock), 0, hs(s), w, g,
+                       lr, n, vec);
+    return launch_status();
+}
+
+}  // extern "C"

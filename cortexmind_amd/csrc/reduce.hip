@@ -1,0 +1,367 @@
+// fp32 reductions sum / mean / max / argmax, flat and over the middle axis
+// of [outer, dim, inner].
+//
+// Replaces avx2::reduce (source/CortexMind/framework/Engine/AVX2/
+// reduce.hpp:49-296, reduce.cpp:17-84, 204-251, 439-528).  Semantics the
+// kernels keep from it are listed in include/cxm_hip.h.
+//
+// Two kernels cover every shape:
+//  * k_rows: inner == 1 (row reductions, and the flat form as one row).
+//    Each row is cut into `segs` segments; one 256-thread workgroup reduces
+//    a segment with 128-bit loads, several in flight per thread, then a DPP
+//    wave reduce and a 4-entry LDS combine.  With segs > 1 the segment
+//    results go to the workspace and the last workgroup of the row combines
+//    them in segment order.
+//  * k_cols: inner > 1.  A workgroup owns 256 adjacent columns of one outer
+//    slice and a chunk of the reduced rows; each thread keeps one float4 of
+//    columns, the four waves take interleaved rows and meet in LDS.  Chunks
+//    are combined in chunk order by the last workgroup of the column tile.
+#include <type_traits>
+
+#include "cxm_common.hpp"
+
+namespace cxm {
+namespace {
+
+// Max over a column path starts from the first slice (reduce.cpp:230-236),
+// which is the same as starting from -inf.
+struct MaxColOp : MaxOp {
+    __device__ static T identity() { return -INFINITY; }
+};
+
+enum OutKind : int { kOutValue = 0, kOutMean = 1, kOutIndex = 2 };
+
+struct OutDesc {
+    void *z;
+    int kind;
+    size_t body;  // mean: outputs [0, body) multiply by inv, the rest divide by dimf
+    float inv;
+    float dimf;
+};
+
+template <class Op>
+__device__ __forceinline__ void write_out(const OutDesc &o, size_t q, typename Op::T r) {
+    if constexpr (std::is_same_v<Op, ArgMaxOp>) {
+        static_cast<int32_t *>(o.z)[q] = r.i;
+    } else {
+        float v = r;
+        if (o.kind == kOutMean) v = q < o.body ? v * o.inv : v / o.dimf;
+        static_cast<float *>(o.z)[q] = v;
+    }
+}
+
+template <class Op>
+__device__ __forceinline__ void fold4(typename Op::T (&acc)[4], const float4 v, int base) {
+    acc[0] = Op::combine(acc[0], Op::from(v.x, base + 0));
+    acc[1] = Op::combine(acc[1], Op::from(v.y, base + 1));
+    acc[2] = Op::combine(acc[2], Op::from(v.z, base + 2));
+    acc[3] = Op::combine(acc[3], Op::from(v.w, base + 3));
+}
+
+// ------------------------------------------------------------------ rows
+
+template <class Op, bool VEC, int UNR>
+__global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, size_t dim,
+                                                 unsigned segs, size_t seg_len,
+                                                 typename Op::T *__restrict__ part,
+                                                 unsigned *__restrict__ counters, OutDesc out) {
+    using T = typename Op::T;
+    __shared__ T lds[kWavesPerBlock];
+    __shared__ int flag;
+
+    const unsigned b = blockIdx.x;
+    const size_t row = b / segs;
+    const unsigned seg = b - static_cast<unsigned>(row) * segs;
+    const float *__restrict__ xr = x + row * dim;
+    const size_t begin = static_cast<size_t>(seg) * seg_len;
+    const size_t end = begin + seg_len < dim ? begin + seg_len : dim;
+    const int tid = threadIdx.x;
+
+    T acc[4] = {Op::identity(), Op::identity(), Op::identity(), Op::identity()};
+    if constexpr (VEC) {
+        const size_t e4 = end / 4;
+        size_t i = begin / 4 + tid;
+        for (; i + (UNR - 1) * kBlock < e4; i += UNR * kBlock) {
+            float4 v[UNR];
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) v[u] = ld4_stream(xr + 4 * (i + u * kBlock));
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], static_cast<int>(4 * (i + u * kBlock)));
+        }
+        for (; i < e4; i += kBlock) fold4<Op>(acc, ld4_stream(xr + 4 * i), static_cast<int>(4 * i));
+    } else {
+        for (size_t i = begin + tid; i < end; i += kBlock)
+            acc[0] = Op::combine(acc[0], Op::from(xr[i], static_cast<int>(i)));
+    }
+    T r = Op::combine(Op::combine(acc[0], acc[1]), Op::combine(acc[2], acc[3]));
+    r = block_reduce<Op, kBlock>(r, lds);
+
+    if (segs == 1) {
+        if (tid == 0) write_out<Op>(out, row, r);
+        return;
+    }
+    if (tid == 0) st_dev(&part[row * segs + seg], r);
+    if (!last_block_ticket(&counters[row], segs, &flag)) return;
+    T a = Op::identity();
+    for (unsigned s = tid; s < segs; s += kBlock) a = Op::combine(a, ld_dev(&part[row * segs + s]));
+    a = block_reduce<Op, kBlock>(a, lds);
+    if (tid == 0) write_out<Op>(out, row, a);
+}
+
+// ------------------------------------------------------------------ cols
+
+constexpr int kColTile = 256;  // columns per workgroup
+
+template <class Op, bool VEC, int UNR>
+__global__ __launch_bounds__(kBlock) void k_cols(const float *__restrict__ x, size_t dim,
+                                                 size_t inner, unsigned ntiles, unsigned chunks,
+                                                 size_t rows_per_chunk,
+                                                 typename Op::T *__restrict__ part,
+                                                 unsigned *__restrict__ counters, OutDesc out) {
+    using T = typename Op::T;
+    __shared__ T lds[kWavesPerBlock][kColTile];
+    __shared__ int flag;
+
+    const unsigned b = blockIdx.x;
+    const unsigned tile = b % ntiles;
+    const unsigned chunk = (b / ntiles) % chunks;
+    const size_t o = b / (static_cast<size_t>(ntiles) * chunks);
+    const int tid = threadIdx.x;
+    const float *__restrict__ xo = x + o * dim * inner;
+    const size_t r0 = chunk * rows_per_chunk;
+    const size_t r1 = r0 + rows_per_chunk < dim ? r0 + rows_per_chunk : dim;
+
+    T mine;  // this thread's column (tile*256 + tid) over the chunk
+    if constexpr (VEC) {
+        const int lane = tid & (kWave - 1);
+        const int w = tid / kWave;
+        const size_t col = static_cast<size_t>(tile) * kColTile + lane * 4;
+        T acc[4] = {Op::identity(), Op::identity(), Op::identity(), Op::identity()};
+        if (col < inner) {
+            const float *__restrict__ xc = xo + col;
+            size_t r = r0 + w;
+            for (; r + (UNR - 1) * kWavesPerBlock < r1; r += UNR * kWavesPerBlock) {
+                float4 v[UNR];
+#pragma unroll
+                for (int u = 0; u < UNR; ++u)
+                    v[u] = ld4_stream(xc + (r + u * kWavesPerBlock) * inner);
+#pragma unroll
+                for (int u = 0; u < UNR; ++u) {
+                    const int ri = static_cast<int>(r + u * kWavesPerBlock);
+                    acc[0] = Op::combine(acc[0], Op::from(v[u].x, ri));
+                    acc[1] = Op::combine(acc[1], Op::from(v[u].y, ri));
+                    acc[2] = Op::combine(acc[2], Op::from(v[u].z, ri));
+                    acc[3] = Op::combine(acc[3], Op::from(v[u].w, ri));
+                }
+            }
+            for (; r < r1; r += kWavesPerBlock) {
+                const float4 v = ld4_stream(xc + r * inner);
+                const int ri = static_cast<int>(r);
+                acc[0] = Op::combine(acc[0], Op::from(v.x, ri));
+                acc[1] = Op::combine(acc[1], Op::from(v.y, ri));
+                acc[2] = Op::combine(acc[2], Op::from(v.z, ri));
+                acc[3] = Op::combine(acc[3], Op::from(v.w, ri));
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) lds[w][lane * 4 + c] = acc[c];
+        __syncthreads();
+        // Wave w held rows r0+w, r0+w+4, ...: combine in wave order.
+        mine = Op::combine(Op::combine(lds[0][tid], lds[1][tid]), Op::combine(lds[2][tid], lds[3][tid]));
+    } else {
+        const size_t col = static_cast<size_t>(tile) * kColTile + tid;
+        mine = Op::identity();
+        if (col < inner)
+            for (size_t r = r0; r < r1; ++r)
+                mine = Op::combine(mine, Op::from(xo[r * inner + col], static_cast<int>(r)));
+    }
+
+    const size_t col = static_cast<size_t>(tile) * kColTile + tid;
+    if (chunks == 1) {
+        if (col < inner) write_out<Op>(out, o * inner + col, mine);
+        return;
+    }
+    const size_t slot = (o * ntiles + tile) * chunks;
+    st_dev(&part[(slot + chunk) * kColTile + tid], mine);
+    if (!last_block_ticket(&counters[o * ntiles + tile], chunks, &flag)) return;
+    T a = Op::identity();
+    for (unsigned c = 0; c < chunks; ++c) a = Op::combine(a, ld_dev(&part[(slot + c) * kColTile + tid]));
+    if (col < inner) write_out<Op>(out, o * inner + col, a);
+}
+
+__global__ void k_fill_f32(float *z, float v) { *z = v; }
+
+// ------------------------------------------------------------------ host
+
+constexpr unsigned kTargetBlocks = 2048;
+
+template <class Op>
+int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t s) {
+    using T = typename Op::T;
+    hipStream_t hs = reinterpret_cast<hipStream_t>(s);
+    const bool vec = aligned16(x) && dim % 4 == 0;
+    // Segment length: a multiple of 256 threads x 4 floats, split so that the
+    // grid has about kTargetBlocks workgroups when there are few rows.
+    size_t segs = 1;
+    if (rows < kTargetBlocks) {
+        const size_t want = (kTargetBlocks + rows - 1) / rows;
+        const size_t max_segs = (dim + 1023) / 1024;
+        segs = want < max_segs ? want : max_segs;
+        if (segs == 0) segs = 1;
+    }
+    size_t seg_len = (dim + segs - 1) / segs;
+    seg_len = (seg_len + 1023) / 1024 * 1024;
+    segs = seg_len ? (dim + seg_len - 1) / seg_len : 1;
+    if (segs == 0) segs = 1;
+    const size_t blocks = rows * segs;
+    if (blocks > 0x7fffffffu) return CXM_E_TOO_LARGE;
+
+    T *part = nullptr;
+    unsigned *counters = nullptr;
+    if (segs > 1) {
+        Workspace ws;
+        int rc = get_workspace(s, rows, rows * segs * sizeof(T), &ws);
+        if (rc) return rc;
+        part = static_cast<T *>(ws.scratch);
+        counters = ws.counters;
+    }
+    const unsigned nb = static_cast<unsigned>(blocks);
+    const size_t per_thread = seg_len / (4 * kBlock);  // float4 loads per thread
+    if (vec && per_thread >= 8)
+        hipLaunchKernelGGL((k_rows<Op, true, 8>), dim3(nb), dim3(kBlock), 0, hs, x, dim,
+                           static_cast<unsigned>(segs), seg_len, part, counters, out);
+    else if (vec)
+        hipLaunchKernelGGL((k_rows<Op, true, 4>), dim3(nb), dim3(kBlock), 0, hs, x, dim,
+                           static_cast<unsigned>(segs), seg_len, part, counters, out);
+    else
+        hipLaunchKernelGGL((k_rows<Op, false, 1>), dim3(nb), dim3(kBlock), 0, hs, x, dim,
+                           static_cast<unsigned>(segs), seg_len, part, counters, out);
+    return launch_status();
+}
+
+template <class Op>
+int run_cols(const float *x, size_t outer, size_t dim, size_t inner, OutDesc out, cxm_stream_t s) {
+    using T = typename Op::T;
+    hipStream_t hs = reinterpret_cast<hipStream_t>(s);
+    const bool vec = aligned16(x) && inner % 4 == 0;
+    const size_t ntiles = (inner + kColTile - 1) / kColTile;
+    const size_t tiles = ntiles * outer;
+    size_t chunks = 1;
+    if (tiles < kTargetBlocks) {
+        const size_t want = (kTargetBlocks / 2 + tiles - 1) / tiles;
+        const size_t max_chunks = (dim + 15) / 16;  // at least 16 rows (4 per wave) per chunk
+        chunks = want < max_chunks ? want : max_chunks;
+        if (chunks == 0) chunks = 1;
+    }
+    size_t rpc = (dim + chunks - 1) / chunks;
+    rpc = (rpc + 3) / 4 * 4;
+    chunks = (dim + rpc - 1) / rpc;
+    if (chunks == 0) chunks = 1;
+    const size_t blocks = tiles * chunks;
+    if (blocks > 0x7fffffffu || ntiles > 0xffffffffu) return CXM_E_TOO_LARGE;
+
+    T *part = nullptr;
+    unsigned *counters = nullptr;
+    if (chunks > 1) {
+        Workspace ws;
+        int rc = get_workspace(s, tiles, tiles * chunks * kColTile * sizeof(T), &ws);
+        if (rc) return rc;
+        part = static_cast<T *>(ws.scratch);
+        counters = ws.counters;
+    }
+    const unsigned nb = static_cast<unsigned>(blocks);
+    if (vec)
+        hipLaunchKernelGGL((k_cols<Op, true, 8>), dim3(nb), dim3(kBlock), 0, hs, x, dim, inner,
+                           static_cast<unsigned>(ntiles), static_cast<unsigned>(chunks), rpc, part,
+                           counters, out);
+    else
+        hipLaunchKernelGGL((k_cols<Op, false, 1>), dim3(nb), dim3(kBlock), 0, hs, x, dim, inner,
+                           static_cast<unsigned>(ntiles), static_cast<unsigned>(chunks), rpc, part,
+                           counters, out);
+    return launch_status();
+}
+
+enum Which { kSum, kMean, kMax, kArgMax };
+
+int reduce_axis(Which which, const float *x, void *z, size_t outer, size_t dim, size_t inner,
+                cxm_stream_t s) {
+    if (!x || !z) return CXM_E_INVALID;
+    if (outer == 0 || inner == 0) return CXM_OK;  // empty output
+    if (dim == 0) return CXM_E_INVALID;
+    if (which == kArgMax && dim > 0x7fffffffu) return CXM_E_TOO_LARGE;
+    const size_t total = outer * inner;
+    OutDesc out{z, which == kMean ? kOutMean : (which == kArgMax ? kOutIndex : kOutValue),
+                total - total % 8, 1.0f / static_cast<float>(dim), static_cast<float>(dim)};
+    if (inner == 1) {
+        switch (which) {
+            case kSum:
+            case kMean: return run_rows<SumOp>(x, outer, dim, out, s);
+            case kMax: return run_rows<MaxOp>(x, outer, dim, out, s);
+            default: return run_rows<ArgMaxOp>(x, outer, dim, out, s);
+        }
+    }
+    switch (which) {
+        case kSum:
+        case kMean: return run_cols<SumOp>(x, outer, dim, inner, out, s);
+        case kMax: return run_cols<MaxColOp>(x, outer, dim, inner, out, s);
+        default: return run_cols<ArgMaxOp>(x, outer, dim, inner, out, s);
+    }
+}
+
+int reduce_flat(Which which, const float *x, void *z, size_t n, cxm_stream_t s) {
+    if (!z) return CXM_E_INVALID;
+    hipStream_t hs = reinterpret_cast<hipStream_t>(s);
+    if (n == 0) {
+        // reduce.cpp:17-28 / 66-69 / 204-215 on zero elements: 0, 0/0, -FLT_MAX.
+        if (which == kArgMax) return CXM_E_INVALID;  // the reference reads x[0]
+        const float v = which == kSum ? 0.0f : (which == kMean ? NAN : -FLT_MAX);
+        hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(1), 0, hs, static_cast<float *>(z), v);
+        return launch_status();
+    }
+    if (!x) return CXM_E_INVALID;
+    if (which == kArgMax && n > 0x7fffffffu) return CXM_E_TOO_LARGE;
+    OutDesc out{z, which == kMean ? kOutMean : (which == kArgMax ? kOutIndex : kOutValue), 0,
+                0.0f, static_cast<float>(n)};
+    switch (which) {
+        case kSum:
+        case kMean: return run_rows<SumOp>(x, 1, n, out, s);
+        case kMax: return run_rows<MaxOp>(x, 1, n, out, s);
+        default: return run_rows<ArgMaxOp>(x, 1, n, out, s);
+    }
+}
+
+}  // namespace
+}  // namespace cxm
+
+extern "C" {
+
+int cxm_reduce_sum_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s) {
+    return cxm::reduce_flat(cxm::kSum, x, z, n, s);
+}
+int cxm_reduce_mean_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s) {
+    return cxm::reduce_flat(cxm::kMean, x, z, n, s);
+}
+int cxm_reduce_max_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s) {
+    return cxm::reduce_flat(cxm::kMax, x, z, n, s);
+}
+int cxm_reduce_argmax_flat_f32(const float *x, int32_t *z, size_t n, cxm_stream_t s) {
+    return cxm::reduce_flat(cxm::kArgMax, x, z, n, s);
+}
+int cxm_reduce_sum_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                       cxm_stream_t s) {
+    return cxm::reduce_axis(cxm::kSum, x, z, outer, dim, inner, s);
+}
+int cxm_reduce_mean_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                        cxm_stream_t s) {
+    return cxm::reduce_axis(cxm::kMean, x, z, outer, dim, inner, s);
+}
+int cxm_reduce_max_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                       cxm_stream_t s) {
+    return cxm::reduce_axis(cxm::kMax, x, z, outer, dim, inner, s);
+}
+int cxm_reduce_argmax_f32(const float *x, int32_t *z, size_t outer, size_t dim, size_t inner,
+                          cxm_stream_t s) {
+    return cxm::reduce_axis(cxm::kArgMax, x, z, outer, dim, inner, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,207 @@
+/*
+ * cxm_hip.h -- C ABI of the CortexMind MI355X (gfx950) backend.
+ *
+ * Plain C: raw pointers, element counts and an opaque stream handle; no
+ * torch, no HIP or CUDA types in the signatures.  Every entry point returns
+ * an int status: CXM_OK (0) on success, a negative CXM_E_* code for an
+ * argument error detected on the host before anything is launched, or a
+ * positive HIP runtime error code.  Kernels launch asynchronously on the
+ * given stream (NULL = the device's null stream); only the d2h copy and the
+ * *_sync calls block the host.
+ *
+ * Ownership follows the reference engine: the caller owns every buffer and
+ * ops write into a preallocated output (reference
+ * source/CortexMind/framework/Engine/AVX2/reduce.hpp:49-329 and
+ * Engine/CUDA/matrix.cuh:11-26: no op allocates its output).  Multi-pass
+ * kernels take their scratch from a per-(device, stream) workspace that the
+ * library allocates on first use and keeps until cxm_release_workspaces();
+ * calls on distinct streams are independent, calls on one stream are ordered.
+ *
+ * Reference paths below are relative to source/CortexMind/framework/.
+ */
+#ifndef CXM_HIP_H
+#define CXM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *cxm_stream_t; /* a hipStream_t; NULL = null stream */
+typedef struct ihipEvent_t *cxm_event_t;   /* a hipEvent_t */
+
+/* ---------------------------------------------------------------- status */
+#define CXM_OK 0
+#define CXM_E_INVALID (-1)     /* null pointer, zero/mismatched size, bad enum */
+#define CXM_E_TOO_LARGE (-2)   /* size beyond what the kernel indexes (int32 argmax etc.) */
+#define CXM_E_NO_DEVICE (-3)   /* no gfx950 device visible */
+
+/* Binary operator codes (Engine/AVX2/broadcast.hpp:29-56, Engine/AVX2/matrix.hpp:38-94). */
+#define CXM_OP_ADD 0
+#define CXM_OP_SUB 1
+#define CXM_OP_MUL 2
+#define CXM_OP_DIV 3
+#define CXM_OP_MAX 4
+#define CXM_OP_MIN 5
+
+/* Activation codes (Engine/AVX2/functions.hpp:186-188 exp, 372-374 relu,
+ * 381-383 tanh, 405-411 sigmoid). */
+#define CXM_ACT_NONE 0
+#define CXM_ACT_RELU 1
+#define CXM_ACT_SIGMOID 2
+#define CXM_ACT_TANH 3
+#define CXM_ACT_EXP 4
+
+/* Human-readable text for a status code (never NULL). */
+const char *cxm_error_string(int status);
+
+/* ------------------------------------------------ device, memory, streams
+ * Replace the reference's device pool and copies:
+ *   ForgeChunk::allocate / deallocate (Memory/forge.cu:28-89),
+ *   transform::upload / download / copy_d2d (Memory/transform.cu:17-40),
+ *   nv::stream (Engine/CUDA/stream.cu:10-43). */
+int cxm_device_count(int *count);
+int cxm_set_device(int device);
+/* Name, compute-unit count and gcn arch string ("gfx950...") of the current device. */
+int cxm_device_info(char *name, size_t name_len, int *cu_count, char *arch, size_t arch_len);
+int cxm_device_sync(void);
+int cxm_dev_malloc(void **ptr, size_t bytes);
+int cxm_dev_free(void *ptr);
+int cxm_memcpy_h2d(void *dst, const void *src, size_t bytes, cxm_stream_t s);
+/* Copies and then waits for the stream, like the reference's blocking download. */
+int cxm_memcpy_d2h(void *dst, const void *src, size_t bytes, cxm_stream_t s);
+int cxm_memcpy_d2d(void *dst, const void *src, size_t bytes, cxm_stream_t s);
+int cxm_memset(void *dst, int byte_value, size_t bytes, cxm_stream_t s);
+int cxm_stream_create(cxm_stream_t *s);
+int cxm_stream_sync(cxm_stream_t s);
+int cxm_stream_destroy(cxm_stream_t s);
+int cxm_event_create(cxm_event_t *e);
+int cxm_event_record(cxm_event_t e, cxm_stream_t s);
+int cxm_event_sync(cxm_event_t e);
+int cxm_event_elapsed_ms(float *ms, cxm_event_t start, cxm_event_t stop);
+int cxm_event_destroy(cxm_event_t e);
+/* Frees every workspace the library holds (waits for their streams first). */
+int cxm_release_workspaces(void);
+
+/* ------------------------------------------------------------ reductions
+ * avx2::reduce (Engine/AVX2/reduce.hpp:49-296, reduce.cpp:17-84,204-251,
+ * 439-528).  The flat form reduces N elements to z[0]; the axis form treats
+ * x as row-major [outer, dim, inner] and writes z[outer, inner].
+ * Semantics kept from the reference:
+ *   max, flat form and inner == 1: starts from -FLT_MAX (reduce.cpp:206),
+ *       so an all -inf row gives -FLT_MAX; inner > 1 starts from slice 0;
+ *   argmax: index (int32) of the first maximum, 0 for an all-equal slice;
+ *   mean, flat: sum / (float)N; axis: the first floor(outer*inner/8)*8
+ *       outputs are sum * rn(1/dim), the rest sum / (float)dim (reduce.cpp:77-83).
+ * Sums are deterministic (fixed tree order) and differ from the reference's
+ * 8-lane sequential order only in rounding. */
+int cxm_reduce_sum_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s);
+int cxm_reduce_mean_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s);
+int cxm_reduce_max_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s);
+int cxm_reduce_argmax_flat_f32(const float *x, int32_t *z, size_t n, cxm_stream_t s);
+int cxm_reduce_sum_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                       cxm_stream_t s);
+int cxm_reduce_mean_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                        cxm_stream_t s);
+int cxm_reduce_max_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                       cxm_stream_t s);
+int cxm_reduce_argmax_f32(const float *x, int32_t *z, size_t outer, size_t dim, size_t inner,
+                          cxm_stream_t s);
+
+/* ------------------------------------------------------------ elementwise
+ * Same-shape binary z = x op y: matrix_t::{add,sub,mul,div,max,min}
+ * (Engine/AVX2/matrix.hpp:38-94) and nv::Matrix (Engine/CUDA/matrix.cuh:12-25).
+ * z may alias x (the in-place forms, matrix.hpp:130-160).  max/min are
+ * (x > y ? x : y) / (x < y ? x : y), as _mm256_max_ps / _mm256_min_ps. */
+int cxm_binary_f32(const float *x, const float *y, float *z, size_t n, int op, cxm_stream_t s);
+/* Row broadcast z[i,j] = x[i,j] op y[j] over [m, n]: Broadcast::row
+ * (Engine/AVX2/broadcast.hpp:28-37).  Column broadcast z[i,j] = x[i,j] op y[i]:
+ * Broadcast::col (broadcast.hpp:47-56).  z may alias x.  op in ADD..DIV. */
+int cxm_bcast_row_f32(const float *x, const float *y, float *z, size_t m, size_t n, int op,
+                      cxm_stream_t s);
+int cxm_bcast_col_f32(const float *x, const float *y, float *z, size_t m, size_t n, int op,
+                      cxm_stream_t s);
+/* Tensor-op-scalar z = x op value: ScalarOp (Engine/AVX2/scalar.cpp:89-119),
+ * nv::ScalarKernel (Engine/CUDA/scalar.cu:16-134).  z may alias x. */
+int cxm_scalar_f32(const float *x, float value, float *z, size_t n, int op, cxm_stream_t s);
+/* z = act(x) for act in RELU, SIGMOID, TANH, EXP (Engine/AVX2/functions.hpp:
+ * 372-374, 405-411, 381-383, 186-188; nv::ElementWise::exp,
+ * Engine/CUDA/element_wise.cu:84-92).  relu(x) = (0 > x) ? 0 : x. */
+int cxm_unary_f32(const float *x, float *z, size_t n, int act, cxm_stream_t s);
+
+/* Fused y = act(x * scale[j] + bias[j]) over [m, n]: Broadcast::row::mul then
+ * Broadcast::row::add in place (broadcast.cpp:206-216, 230-240), then the
+ * activation; the product and the sum are rounded separately (no fma). */
+int cxm_affine_act_fwd_f32(const float *x, const float *scale, const float *bias, float *y,
+                           size_t m, size_t n, int act, cxm_stream_t s);
+/* Backward of the above from the saved output y: g = act'(y) (relu: y > 0,
+ * sigmoid: y*(1-y), tanh: 1-y*y), dz = dy*g, dx = dz*scale[j],
+ * dscale[j] = sum_i dz*x, dbias[j] = sum_i dz.  No reference counterpart
+ * (the reference has no backward); composed of matrix_t::mul,
+ * Broadcast::row::mul and reduce::sum over axis 0. */
+int cxm_affine_act_bwd_f32(const float *x, const float *scale, const float *y, const float *dy,
+                           float *dx, float *dscale, float *dbias, size_t m, size_t n, int act,
+                           cxm_stream_t s);
+
+/* --------------------------------------------------------------- softmax
+ * Row softmax (log_mode = 0) or log-softmax (log_mode = 1) over the last axis
+ * of [rows, cols].  The reference has none; it is the composition
+ * m = reduce::max (reduce.cpp:204-215), z = Broadcast::col::sub(x, m),
+ * e = exp(z), s = reduce::sum(e), y = Broadcast::col::div(e, s) or z - log(s).
+ * -inf entries give exactly 0 (softmax) and -inf (log-softmax). */
+int cxm_softmax_fwd_f32(const float *x, float *y, size_t rows, size_t cols, int log_mode,
+                        cxm_stream_t s);
+/* Backward from the saved output y: softmax dx = y*(dy - sum(dy*y));
+ * log-softmax dx = dy - exp(y)*sum(dy). */
+int cxm_softmax_bwd_f32(const float *y, const float *dy, float *dx, size_t rows, size_t cols,
+                        int log_mode, cxm_stream_t s);
+
+/* ---------------------------------------------------------------- matmul
+ * Row-major C[xN, zN] = A[xN, yN] * B[yN, zN]: matrix_t::matmul
+ * (Engine/AVX2/matrix.hpp:119, matrix.cpp:75-147) and nv::Matrix::matmul
+ * (Engine/CUDA/matrix.cu:112-159, which uses TF32; this one is true fp32 on
+ * v_mfma_f32_32x32x2_f32). */
+int cxm_matmul_f32(const float *a, const float *b, float *c, size_t xN, size_t yN, size_t zN,
+                   cxm_stream_t s);
+/* General form: C[m,n] = op(A)[m,k] * op(B)[k,n], then the epilogue.
+ * A is stored [m,k] ([k,m] when trans_a), B is [k,n] ([n,k] when trans_b).
+ * bias (length n, or NULL) is added to every row; act is NONE or RELU;
+ * gate (an [m,n] array, or NULL) multiplies the result by (gate > 0 ? 1 : 0),
+ * which is the ReLU backward from the saved activation.  No reference
+ * counterpart for the transposed and fused forms (matrix.cpp has only NN). */
+int cxm_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t k, size_t n,
+                 int trans_a, int trans_b, const float *bias, int act, const float *gate,
+                 cxm_stream_t s);
+
+/* ----------------------------------------------------------- training step
+ * Softmax cross-entropy on logits [b, c] with int32 labels in [0, c):
+ * loss[0] = mean_r(-log_softmax(logits)[r, label_r]) and
+ * dlogits = (softmax(logits) - onehot) / b.  No reference counterpart. */
+int cxm_softmax_xent_f32(const float *logits, const int32_t *labels, float *loss, float *dlogits,
+                         size_t b, size_t c, cxm_stream_t s);
+/* w -= lr * g, as matrix_t::sub(w, ScalarOp::mul(g, lr)): two roundings. */
+int cxm_sgd_f32(float *w, const float *g, float lr, size_t n, cxm_stream_t s);
+
+/* ------------------------------------------------------------- MLP step
+ * One SGD training step of a 3-layer ReLU MLP, d0 -> d1 -> d2 -> d3, on a
+ * batch of `batch` rows: forward, softmax cross-entropy on int32 labels,
+ * reverse-mode backward, then W -= lr*gW and b -= lr*gb for all six
+ * parameters (weights stored [fan_in, fan_out], row-major).  No reference
+ * counterpart: the reference's autograd has only the abstract
+ * meta::GradientFlow::backward (Graph/flow.hpp:15-24) and no layers, loss or
+ * optimizer; this is the step its concrete flows would perform.
+ * The handle owns the activations and gradients (allocated once). */
+typedef struct cxm_mlp3 cxm_mlp3;
+int cxm_mlp3_create(cxm_mlp3 **handle, size_t batch, size_t d0, size_t d1, size_t d2, size_t d3);
+int cxm_mlp3_step_f32(cxm_mlp3 *handle, const float *x, const int32_t *labels, float *w1, float *b1,
+                      float *w2, float *b2, float *w3, float *b3, float lr, float *loss,
+                      cxm_stream_t s);
+int cxm_mlp3_destroy(cxm_mlp3 *handle);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CXM_HIP_H */

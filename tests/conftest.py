@@ -18,3 +18,17 @@ def orc():
 
     oracle.lib()
     return oracle
+
+
+@pytest.fixture(scope="session")
+def hip():
+    """The loaded gfx950 library with a device; fails (never skips) when a
+    GPU test runs without one, so a missing backend cannot pass silently."""
+    from cortexmind_amd import _lib
+    from cortexmind_amd.device import device_count, device_info
+
+    _lib.lib()
+    assert device_count() >= 1, "GPU test run without a visible HIP device"
+    info = device_info()
+    assert "gfx950" in info["arch"], f"expected gfx950, got {info}"
+    return _lib

@@ -1,0 +1,81 @@
+"""CPU-only checks of the C ABI boundary: the library loads, exports every
+function include/cxm_hip.h declares, and rejects bad arguments on the host
+(before any HIP call, so these run without a GPU)."""
+import ctypes
+import numpy as np
+import pytest
+
+from cortexmind_amd import _lib
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    declared = _lib.header_symbols()
+    assert len(declared) >= 40
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert missing == []
+    # and the Python binding declares a signature for each of them
+    unbound = [s for s in declared if s not in _lib.SIGNATURES and s != "cxm_error_string"]
+    assert unbound == []
+
+
+def test_library_carries_gfx950_device_code():
+    data = open(_lib.LIB_PATH, "rb").read()
+    assert b"amdgcn-amd-amdhsa--gfx950" in data
+
+
+def test_abi_header_is_plain_c():
+    import re
+
+    text = open(_lib.HEADER).read()
+    code = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    assert re.findall(r"#include\s*<([^>]+)>", code) == ["stddef.h", "stdint.h"]
+    for word in ("torch", "cuda", "hip_", "Tensor", "template", "class "):
+        assert word not in code
+
+
+def test_error_strings():
+    lib = _lib.lib()
+    assert lib.cxm_error_string(0) == b"success"
+    assert b"invalid" in lib.cxm_error_string(_lib.E_INVALID)
+    assert lib.cxm_error_string(-99) == b"unknown cxm status"
+
+
+@pytest.mark.parametrize("fn,args", [
+    ("cxm_reduce_sum_f32", (None, None, 4, 4, 1, None)),
+    ("cxm_reduce_argmax_flat_f32", (None, None, 0, None)),
+    ("cxm_binary_f32", (None, None, None, 4, 0, None)),
+    ("cxm_bcast_row_f32", (None, None, None, 4, 4, 0, None)),
+    ("cxm_scalar_f32", (None, 1.0, None, 4, 0, None)),
+    ("cxm_unary_f32", (None, None, 4, 1, None)),
+    ("cxm_affine_act_fwd_f32", (None, None, None, None, 4, 4, 1, None)),
+    ("cxm_affine_act_bwd_f32", (None,) * 7 + (4, 4, 1, None)),
+    ("cxm_softmax_fwd_f32", (None, None, 4, 4, 0, None)),
+    ("cxm_softmax_bwd_f32", (None, None, None, 4, 4, 0, None)),
+    ("cxm_gemm_f32", (None, None, None, 4, 4, 4, 0, 0, None, 0, None, None)),
+    ("cxm_matmul_f32", (None, None, None, 4, 4, 4, None)),
+    ("cxm_softmax_xent_f32", (None, None, None, None, 4, 4, None)),
+    ("cxm_sgd_f32", (None, None, 0.1, 4, None)),
+    ("cxm_mlp3_step_f32", (None,) * 9 + (0.1, None, None)),
+])
+def test_null_pointers_rejected_on_host(fn, args):
+    assert getattr(_lib.lib(), fn)(*args) == _lib.E_INVALID
+
+
+def test_bad_enums_rejected_on_host():
+    lib = _lib.lib()
+    p = ctypes.c_void_p(0x1000)  # never dereferenced: the enum check comes first
+    assert lib.cxm_binary_f32(p, p, p, 4, 9, None) == _lib.E_INVALID
+    assert lib.cxm_bcast_col_f32(p, p, p, 4, 4, _lib.OP_MAX, None) == _lib.E_INVALID
+    assert lib.cxm_unary_f32(p, p, 4, 17, None) == _lib.E_INVALID
+    assert lib.cxm_softmax_fwd_f32(p, p, 4, 4, 2, None) == _lib.E_INVALID
+    assert lib.cxm_gemm_f32(p, p, p, 4, 4, 4, 0, 0, None, _lib.ACT_SIGMOID, None, None) == _lib.E_INVALID
+
+
+def test_empty_outputs_are_noops():
+    lib = _lib.lib()
+    p = ctypes.c_void_p(0x1000)
+    assert lib.cxm_reduce_sum_f32(p, p, 0, 5, 3, None) == 0
+    assert lib.cxm_binary_f32(p, p, p, 0, 0, None) == 0
+    assert lib.cxm_softmax_fwd_f32(p, p, 0, 8, 0, None) == 0
+    assert lib.cxm_gemm_f32(p, p, p, 0, 4, 4, 0, 0, None, 0, None, None) == 0

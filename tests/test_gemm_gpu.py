@@ -1,0 +1,93 @@
+"""Parity of the gfx950 fp32 MFMA GEMM with the CPU oracle (a restatement of
+matrix_t::matmul, source/CortexMind/framework/Engine/AVX2/matrix.cpp:75-147,
+plus transposed copies for the forms the reference lacks).
+
+Bar: |gpu - ref| <= 1e-5 * (|A| |B|)_ij per element (summation order
+differs; both are fp32).  Epilogues (bias add, ReLU, ReLU gate) are exact
+operations applied after the sum.
+"""
+import numpy as np
+import pytest
+
+from cortexmind_amd import engine
+from cortexmind_amd._lib import ACT_NONE, ACT_RELU, E_INVALID, lib
+from cortexmind_amd.data import SplitMix64
+
+from gpu_util import dev, empty
+
+pytestmark = pytest.mark.gpu
+
+
+def stored(a, trans):
+    return np.ascontiguousarray(a.T) if trans else a
+
+
+def run(a_op, b_op, ta, tb, bias=None, act=ACT_NONE, gate=None):
+    m, k = a_op.shape
+    n = b_op.shape[1]
+    da, db = dev(stored(a_op, ta)), dev(stored(b_op, tb))
+    dc = empty((m, n))
+    engine.gemm(da, db, dc, m, k, n, ta, tb, bias=dev(bias) if bias is not None else None, act=act,
+                gate=dev(gate) if gate is not None else None)
+    return dc.numpy()
+
+
+def bound(a_op, b_op):
+    return 1e-5 * (np.abs(a_op.astype(np.float64)) @ np.abs(b_op.astype(np.float64))) + 1e-30
+
+
+SHAPES = [(128, 128, 128), (64, 32, 48), (33, 17, 65), (1, 1, 1), (256, 784, 1024),
+          (512, 1024, 10), (1024, 512, 10), (300, 10, 1024), (784, 2048, 1024), (130, 4100, 7)]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES, ids=lambda v: str(v))
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_gemm_vs_oracle(hip, orc, m, k, n, ta, tb):
+    g = SplitMix64(m * 7919 + k * 31 + n + 1000 * ta + 2000 * tb)
+    a = g.normal((m, k))
+    b = g.normal((k, n))
+    got = run(a, b, ta, tb)
+    ref = orc.gemm(stored(a, ta), stored(b, tb), bool(ta), bool(tb))
+    assert np.all(np.abs(got - ref) <= bound(a, b))
+
+
+def test_matmul_mirror_name(hip, orc):
+    g = SplitMix64(9)
+    a, b = g.uniform((100, 60), -1, 1), g.uniform((60, 36), -1, 1)
+    da, db, dc = dev(a), dev(b), empty((100, 36))
+    engine.matrix_t.matmul(da, db, dc, 100, 60, 36)
+    assert np.all(np.abs(dc.numpy() - orc.matmul(a, b)) <= bound(a, b))
+
+
+@pytest.mark.parametrize("m,k,n", [(4096, 784, 1024), (4096, 1024, 1024), (1024, 4096, 1024)])
+def test_gemm_full_size_float64(hip, m, k, n):
+    """C5's large products at full size, against float64 numpy."""
+    g = SplitMix64(m + k + n)
+    a = g.uniform((m, k), 0.0, 1.0)
+    b = g.normal((k, n), 0.0, float(np.sqrt(2.0 / k)))
+    got = run(a, b, 0, 0)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.all(np.abs(got - ref) <= bound(a, b))
+
+
+def test_epilogue_bias_relu_gate(hip, orc):
+    g = SplitMix64(17)
+    a, b = g.normal((200, 96)), g.normal((96, 72))
+    bias = g.normal((72,), 0.0, 0.5)
+    z = orc.bcast_row(orc.matmul(a, b), bias, 0)
+    got = run(a, b, 0, 0, bias=bias, act=ACT_RELU)
+    tol = bound(a, b)
+    relu_ref = np.where(0 > z, 0, z)
+    assert np.all(np.abs(got - relu_ref) <= tol)
+    assert np.all(got >= 0)
+    gate = g.normal((200, 72))
+    got_g = run(a, b, 0, 0, gate=gate)
+    ref_g = orc.matmul(a, b) * (gate > 0)
+    assert np.all(np.abs(got_g - ref_g) <= tol)
+    assert np.all(got_g[gate <= 0] == 0)
+
+
+def test_bad_arguments(hip):
+    assert lib().cxm_gemm_f32(None, None, None, 4, 4, 4, 0, 0, None, 0, None, None) == E_INVALID
+    d = empty((16,))
+    assert lib().cxm_gemm_f32(d.ptr, d.ptr, d.ptr, 4, 4, 4, 0, 0, None, 7, None, None) == E_INVALID
