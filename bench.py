@@ -3,23 +3,28 @@
 
 Default workload (the config BASELINE's metric is quoted on): C2, the
 reductions on fp32 [4096, 4096] ~ U(-1, 1).  One step = the ten reductions
-of that config, each a separate kernel launch reading a 64 MiB input:
-global sum, global mean, and per-row (axis 1) and per-column (axis 0)
-sum / mean / max / argmax.  Inputs rotate over ten device buffers (640 MiB,
-more than twice the 256 MiB Infinity Cache), so every launch reads HBM.
+of that config, each one kernel launch reading a 64 MiB input: global sum,
+global mean, and per-row (axis 1) and per-column (axis 0) sum / mean / max /
+argmax.  Inputs rotate over ten device buffers (640 MiB, more than twice the
+256 MiB Infinity Cache), so every launch reads HBM, not the cache.
 
-``value`` = algorithmic bytes of all launches in the timed steps / wall time
-of those steps (HIP events on the launch stream around the K steps, inputs
-resident in HBM before timing starts).  Algorithmic bytes count each input
-element read once and each output written once.  ``roofline`` is for the
-kernel with the largest total time: its algorithmic bytes per launch over
-its average launch time, each launch bracketed by its own pair of events.
+``value`` = algorithmic bytes of the timed steps / their wall time, from
+HIP events on the launch stream around the K steps (inputs resident in HBM
+before timing starts).  Algorithmic bytes count each input element read once
+and each output written once; re-reads are not credited.  ``roofline`` is
+for the kernel with the largest share of step time: algorithmic bytes per
+launch over its average launch time, from events around a run of K
+back-to-back launches of that op alone (rotating inputs).  ``traffic`` is
+the HBM bytes per launch measured with rocprofv3 PMC counters (FETCH_SIZE,
+WRITE_SIZE, scaled against a plain copy kernel), read from
+profiles/pmc_traffic.txt when that file has a line for the kernel.
 ``cpu_baseline`` times the C restatement of the reference AVX2 path
-(oracle/, single thread, as the reference is single-threaded) on the box's
-host CPU over a bounded sample of whole steps.
+(oracle/, one thread, as the reference is single-threaded) on the same host
+over a bounded sample of whole steps.
 
-Other workloads (--workload c1|c3|c4|c5) are for profiling; the default
-run also reports their headline figures under "workloads".
+The default run also reports the other workloads (C1 softmax, C3 affine
+fwd/bwd, C4 long-row softmax fwd/bwd, C5 MLP training step) under
+"workloads"; --workload cN makes one of them the headline, for profiling.
 """
 from __future__ import annotations
 
@@ -35,8 +40,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, published
-PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 MFMA, published
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 matrix, published
 METRIC = "achieved HBM GB/s (% of peak) for fp32 softmax/reductions on 1 MI355X"
+MLP_FLOP_PER_STEP = 39_174_799_360
 
 
 def parse():
@@ -48,47 +54,237 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip the other workloads")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="first copy 64 MiB device-to-device three times (the known-size "
+                        "kernel that scales FETCH_SIZE / WRITE_SIZE counters)")
     return p.parse_args()
 
 
-class Launch:
-    """One kernel launch of a step: a callable plus its algorithmic bytes/flops."""
+class Op:
+    """One op of a step: fn(k) launches it on input rotation slot k."""
 
     def __init__(self, name, kernel, fn, work, unit="B"):
         self.name, self.kernel, self.fn, self.work, self.unit = name, kernel, fn, work, unit
 
 
-def c2_launches(engine, DeviceArray, nbuf=10):
+# ---------------------------------------------------------------- workloads
+
+def wl_c2(E, D):
     from cortexmind_amd.data import c2_reduce
 
     x = c2_reduce()
     rows, cols = x.shape
     n = x.size
-    bufs = [DeviceArray.from_numpy(x) for _ in range(nbuf)]
-    z1 = DeviceArray((1,), np.float32)
-    zf = DeviceArray((4096,), np.float32)
-    zi = DeviceArray((4096,), np.int32)
+    nbuf = 10
+    bufs = [D.from_numpy(x) for _ in range(nbuf)]
+    z1, zf, zi = D((1,), np.float32), D((4096,), np.float32), D((4096,), np.int32)
     xb = 4 * n
+    R = E.reduce
+
+    def rot(f):
+        return lambda k: f(bufs[k % nbuf])
+
     ops = [
-        ("sum_global", "k_rows<SumOp,seg>", lambda b: engine.reduce.sum(b, z1, n), xb + 4),
-        ("mean_global", "k_rows<SumOp,seg>", lambda b: engine.reduce.mean(b, z1, n), xb + 4),
-        ("sum_axis1", "k_rows<SumOp>", lambda b: engine.reduce.sum(b, zf, rows, cols, 1), xb + 4 * rows),
-        ("mean_axis1", "k_rows<SumOp>", lambda b: engine.reduce.mean(b, zf, rows, cols, 1), xb + 4 * rows),
-        ("max_axis1", "k_rows<MaxOp>", lambda b: engine.reduce.max(b, zf, rows, cols, 1), xb + 4 * rows),
-        ("argmax_axis1", "k_rows<ArgMaxOp>", lambda b: engine.reduce.argmax(b, zi, rows, cols, 1), xb + 4 * rows),
-        ("sum_axis0", "k_cols<SumOp>", lambda b: engine.reduce.sum(b, zf, 1, rows, cols), xb + 4 * cols),
-        ("mean_axis0", "k_cols<SumOp>", lambda b: engine.reduce.mean(b, zf, 1, rows, cols), xb + 4 * cols),
-        ("max_axis0", "k_cols<MaxColOp>", lambda b: engine.reduce.max(b, zf, 1, rows, cols), xb + 4 * cols),
-        ("argmax_axis0", "k_cols<ArgMaxOp>", lambda b: engine.reduce.argmax(b, zi, 1, rows, cols), xb + 4 * cols),
+        Op("sum_global", "k_rows<SumOp,true,8>", rot(lambda b: R.sum(b, z1, n)), xb + 4),
+        Op("mean_global", "k_rows<SumOp,true,8>", rot(lambda b: R.mean(b, z1, n)), xb + 4),
+        Op("sum_axis1", "k_rows<SumOp,true,4>", rot(lambda b: R.sum(b, zf, rows, cols, 1)), xb + 4 * rows),
+        Op("mean_axis1", "k_rows<SumOp,true,4>", rot(lambda b: R.mean(b, zf, rows, cols, 1)), xb + 4 * rows),
+        Op("max_axis1", "k_rows<MaxOp,true,4>", rot(lambda b: R.max(b, zf, rows, cols, 1)), xb + 4 * rows),
+        Op("argmax_axis1", "k_rows<ArgMaxOp,true,4>", rot(lambda b: R.argmax(b, zi, rows, cols, 1)), xb + 4 * rows),
+        Op("sum_axis0", "k_cols<SumOp,true,8,16>", rot(lambda b: R.sum(b, zf, 1, rows, cols)), xb + 4 * cols),
+        Op("mean_axis0", "k_cols<SumOp,true,8,16>", rot(lambda b: R.mean(b, zf, 1, rows, cols)), xb + 4 * cols),
+        Op("max_axis0", "k_cols<MaxColOp,true,8,16>", rot(lambda b: R.max(b, zf, 1, rows, cols)), xb + 4 * cols),
+        Op("argmax_axis0", "k_cols<ArgMaxOp,true,8,16>", rot(lambda b: R.argmax(b, zi, 1, rows, cols)), xb + 4 * cols),
     ]
-    keep = (bufs, z1, zf, zi)
-    launches = []
-    for i, (name, kern, fn, work) in enumerate(ops):
-        launches.append(Launch(name, kern, (lambda fn=fn, i=i: (lambda step: fn(bufs[(step * 10 + i) % nbuf])))(), work))
     desc = {"workload": "C2 reductions fp32 [4096,4096] ~ U(-1,1)", "shape": [rows, cols],
-            "ops": [o[0] for o in ops], "rotating_input_buffers": nbuf,
-            "buffer_bytes": xb}
-    return launches, desc, keep, x
+            "ops": [o.name for o in ops], "rotating_input_buffers": nbuf, "buffer_bytes": xb}
+    return ops, desc, (bufs, z1, zf, zi), x
+
+
+def wl_c1(E, D):
+    from cortexmind_amd.data import c1_softmax
+
+    x = c1_softmax()
+    r, c = x.shape
+    nbuf = 128  # 2 MiB each: 256 MiB of inputs and 256 MiB of outputs rotate
+    xs = [D.from_numpy(x) for _ in range(nbuf)]
+    ys = [D((r, c)) for _ in range(nbuf)]
+    ops = [Op("softmax_fwd", "k_sm_fwd_wave<4,false>",
+              lambda k: E.softmax.forward(xs[k % nbuf], ys[k % nbuf], r, c), 2 * 4 * x.size)]
+    desc = {"workload": "C1 row softmax fp32 [512,1024] N(0,1)*4", "shape": [r, c],
+            "rotating_input_buffers": nbuf}
+    return ops, desc, (xs, ys), x
+
+
+def wl_c3(E, D):
+    from cortexmind_amd.data import c3_affine
+
+    x, s, b, dy = c3_affine()
+    m, n = x.shape
+    dx_, ds_, db_, dy_ = D.from_numpy(x), D.from_numpy(s), D.from_numpy(b), D.from_numpy(dy)
+    y_, dX, dS, dB = D((m, n)), D((m, n)), D((n,)), D((n,))
+    A = E.activation
+    big = 4 * m * n
+    ops = []
+    for act, nm in [(E.ACT_RELU, "relu"), (E.ACT_SIGMOID, "sigmoid"), (E.ACT_TANH, "tanh")]:
+        ops.append(Op(f"fwd_{nm}", f"k_affine_fwd_vec<{nm}>",
+                      lambda k, act=act: A.affine_fwd(dx_, ds_, db_, y_, m, n, act), 2 * big + 2 * 4 * n))
+    for act, nm in [(E.ACT_RELU, "relu"), (E.ACT_SIGMOID, "sigmoid"), (E.ACT_TANH, "tanh")]:
+        ops.append(Op(f"bwd_{nm}", f"k_affine_bwd<{nm}>",
+                      lambda k, act=act: A.affine_bwd(dx_, ds_, y_, dy_, dX, dS, dB, m, n, act),
+                      4 * big + 3 * 4 * n))
+    desc = {"workload": "C3 Y=act(X*scale+bias) fp32 [8192,8192], fwd+bwd, act in relu/sigmoid/tanh",
+            "shape": [m, n], "working_set_bytes": 4 * big}
+    return ops, desc, (dx_, ds_, db_, dy_, y_, dX, dS, dB), None
+
+
+def wl_c4(E, D):
+    from cortexmind_amd.data import c4_long_softmax
+
+    x, dy = c4_long_softmax()
+    r, c = x.shape
+    nset = 4
+    X = [D.from_numpy(x) for _ in range(nset)]
+    G = [D.from_numpy(dy) for _ in range(nset)]
+    Y = [D((r, c)) for _ in range(nset)]
+    dX = [D((r, c)) for _ in range(nset)]
+    big = 4 * x.size
+    S = E.softmax
+    ops = [
+        Op("softmax_fwd", "k_sm_fwd_part+apply", lambda k: S.forward(X[k % nset], Y[k % nset], r, c), 2 * big),
+        Op("logsoftmax_fwd", "k_sm_fwd_part+apply<log>", lambda k: S.forward(X[k % nset], Y[k % nset], r, c, log=True), 2 * big),
+        Op("softmax_bwd", "k_sm_bwd_part+apply", lambda k: S.backward(Y[k % nset], G[k % nset], dX[k % nset], r, c), 3 * big),
+        Op("logsoftmax_bwd", "k_sm_bwd_part+apply<log>", lambda k: S.backward(Y[k % nset], G[k % nset], dX[k % nset], r, c, log=True), 3 * big),
+    ]
+    desc = {"workload": "C4 long-row softmax/log-softmax fwd+bwd fp32 [64,131072] N(0,1)*8, 10% -inf",
+            "shape": [r, c], "rotating_sets": nset}
+    return ops, desc, (X, G, Y, dX), None
+
+
+def wl_c5(E, D):
+    from cortexmind_amd.data import c5_mlp
+
+    x, labels, params = c5_mlp()
+    B, d0 = x.shape
+    d1, d2, d3 = params["w1"].shape[1], params["w2"].shape[1], params["w3"].shape[1]
+    dx_, dl_ = D.from_numpy(x), D.from_numpy(labels)
+    P = {k: D.from_numpy(v) for k, v in params.items()}
+    loss = D((1,))
+    net = E.Mlp3(B, d0, d1, d2, d3)
+    ops = [Op("mlp_step", "cxm_mlp3_step", lambda k: net.step(dx_, dl_, P, 0.01, loss),
+              MLP_FLOP_PER_STEP, unit="FLOP")]
+    # the step's largest GEMM alone, for the MFMA roofline
+    h1, w2, h2 = D((B, d1)), P["w2"], D((B, d2))
+    gemm_op = Op("gemm_fwd_4096x1024x1024", "k_gemm<NN>",
+                 lambda k: E.gemm(h1, w2, h2, B, d1, d2), 2 * B * d1 * d2, unit="FLOP")
+    desc = {"workload": "C5 MLP 784-1024-1024-10 fp32 train step, batch 4096, SGD lr 0.01",
+            "flop_per_step": MLP_FLOP_PER_STEP}
+    return ops, desc, (dx_, dl_, P, loss, net, h1, h2, gemm_op), None
+
+
+WORKLOADS = {"c1": wl_c1, "c2": wl_c2, "c3": wl_c3, "c4": wl_c4, "c5": wl_c5}
+
+
+# ------------------------------------------------------------------ timing
+
+def time_steps(ops, steps, warmup, Event, sync):
+    """Whole steps: warm-up, then events around `steps` steps."""
+    k = 0
+    for _ in range(warmup):
+        for o in ops:
+            o.fn(k)
+            k += 1
+    sync()
+    t0, t1 = Event(), Event()
+    t0.record()
+    for _ in range(steps):
+        for o in ops:
+            o.fn(k)
+            k += 1
+    t1.record()
+    t1.sync()
+    ms = t0.elapsed_ms(t1)
+    t0.close()
+    t1.close()
+    return ms
+
+
+def time_op(op, launches, Event, sync):
+    """Average time of one op from events around `launches` back-to-back
+    launches of it alone (inputs rotating)."""
+    for k in range(2):
+        op.fn(k)
+    sync()
+    t0, t1 = Event(), Event()
+    t0.record()
+    for k in range(launches):
+        op.fn(k)
+    t1.record()
+    t1.sync()
+    ms = t0.elapsed_ms(t1) / launches
+    t0.close()
+    t1.close()
+    return ms
+
+
+def rate(work, ms, unit):
+    return work / (ms * 1e-3) / (1e9 if unit == "B" else 1e12)
+
+
+def read_traffic():
+    """kernel -> (fetch_bytes, write_bytes) per launch from profiles/pmc_traffic.txt."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.txt")
+    out = {}
+    if os.path.exists(path):
+        for line in open(path):
+            parts = line.split()
+            if len(parts) >= 3 and not line.startswith("#"):
+                try:
+                    out[parts[0]] = (float(parts[1]), float(parts[2]))
+                except ValueError:
+                    pass
+    return out
+
+
+def run_workload(name, steps, warmup, E, D, Event, sync):
+    ops, desc, keep, host = WORKLOADS[name](E, D)
+    total_ms = time_steps(ops, steps, warmup, Event, sync)
+    step_work = sum(o.work for o in ops)
+    unit = ops[0].unit
+    per_op = {}
+    for o in ops:
+        ms = time_op(o, steps, Event, sync)
+        per_op[o.name] = {"avg_ms": round(ms, 5), ("GB/s" if o.unit == "B" else "TFLOP/s"): round(rate(o.work, ms, o.unit), 2)}
+    extra_ops = [x for x in keep if isinstance(x, Op)]
+    for o in extra_ops:
+        ms = time_op(o, steps, Event, sync)
+        per_op[o.name] = {"avg_ms": round(ms, 5), "TFLOP/s": round(rate(o.work, ms, o.unit), 2)}
+    # dominant kernel: the one with the largest share of step time (C5: the
+    # step's largest GEMM, timed alone)
+    if not extra_ops:
+        by_kernel = {}
+        for o in ops:
+            by_kernel.setdefault(o.kernel, []).append(o)
+        kern, group = max(by_kernel.items(), key=lambda kv: sum(per_op[o.name]["avg_ms"] for o in kv[1]))
+        avg_ms = float(np.mean([per_op[o.name]["avg_ms"] for o in group]))
+        work = float(np.mean([o.work for o in group]))
+        dunit = group[0].unit
+    else:
+        dom = extra_ops[0]
+        kern, avg_ms, work, dunit = dom.kernel, per_op[dom.name]["avg_ms"], dom.work, dom.unit
+    achieved = rate(work, avg_ms, dunit)
+    if dunit == "B":
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4)}
+    else:
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4)}
+    tr = read_traffic().get(kern)
+    roof.update({"traffic": (tr[0] + tr[1]) if tr else None, "kernel": kern,
+                 "avg_launch_ms": round(avg_ms, 5), "algorithmic_per_launch": work})
+    value = rate(step_work * steps, total_ms, unit)
+    return {"value": value, "unit": "GB/s" if unit == "B" else "TFLOP/s", "ms_per_step": total_ms / steps,
+            "config": desc, "roofline": roof, "per_op": per_op, "host": host}
 
 
 def cpu_c2(x, seconds):
@@ -115,78 +311,21 @@ def cpu_c2(x, seconds):
     dt = time.perf_counter() - t0
     return {"value": round(bytes_step * nsteps / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
             "kind": "port",
-            "sample": f"{nsteps} whole C2 steps (10 reductions of fp32 [4096,4096]) "
-                      f"in {dt:.1f} s, oracle/cxm_oracle.c -O3 -mavx2 -mfma, 1 thread"}
-
-
-def time_launches(launches, steps, warmup, stream_sync, Event):
-    """Warm up, then time `steps` steps: one event pair per launch plus an
-    event pair around the whole timed region."""
-    for s in range(warmup):
-        for l in launches:
-            l.fn(s)
-    stream_sync()
-    nl = len(launches)
-    ev = [[(Event(), Event()) for _ in range(nl)] for _ in range(steps)]
-    t_start, t_stop = Event(), Event()
-    stream_sync()
-    t_start.record()
-    for s in range(steps):
-        for i, l in enumerate(launches):
-            ev[s][i][0].record()
-            l.fn(warmup + s)
-            ev[s][i][1].record()
-    t_stop.record()
-    t_stop.sync()
-    stream_sync()
-    total_ms = t_start.elapsed_ms(t_stop)
-    per = [[ev[s][i][0].elapsed_ms(ev[s][i][1]) for s in range(steps)] for i in range(nl)]
-    for row in ev:
-        for a, b in row:
-            a.close()
-            b.close()
-    t_start.close()
-    t_stop.close()
-    return total_ms, per
-
-
-def summarize(launches, total_ms, per, steps):
-    per_op = {}
-    by_kernel = {}
-    for l, times in zip(launches, per):
-        avg = float(np.mean(times))
-        rate = l.work / (avg * 1e-3) / (1e9 if l.unit == "B" else 1e12)
-        per_op[l.name] = {"avg_ms": round(avg, 5), ("GB/s" if l.unit == "B" else "TFLOP/s"): round(rate, 2)}
-        k = by_kernel.setdefault(l.kernel, {"time": 0.0, "work": 0.0, "n": 0, "unit": l.unit})
-        k["time"] += float(np.sum(times))
-        k["work"] += l.work * len(times)
-        k["n"] += len(times)
-    dom_name, dom = max(by_kernel.items(), key=lambda kv: kv[1]["time"])
-    avg_ms = dom["time"] / dom["n"]
-    work_per_launch = dom["work"] / dom["n"]
-    if dom["unit"] == "B":
-        achieved = work_per_launch / (avg_ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4)}
-    else:
-        achieved = work_per_launch / (avg_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4)}
-    roof.update({"traffic": None, "kernel": dom_name, "avg_launch_ms": round(avg_ms, 5),
-                 "algorithmic_per_launch": work_per_launch})
-    return per_op, roof
+            "sample": f"{nsteps} whole C2 steps (10 reductions of fp32 [4096,4096]) in {dt:.1f} s, "
+                      f"oracle/cxm_oracle.c -O3 -mavx2 -mfma, 1 thread"}
 
 
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
-                          "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU only (every GPU box here has one); "
+                                   "--gpus must be 1", "n_gpus": args.gpus}))
         sys.exit(2)
 
-    from cortexmind_amd import engine
-    from cortexmind_amd.device import DeviceArray, Event, device_count, device_info
+    from cortexmind_amd import engine as E
     from cortexmind_amd._lib import call
+    from cortexmind_amd.device import DeviceArray as D
+    from cortexmind_amd.device import Event, device_count, device_info
 
     if device_count() < 1:
         print(json.dumps({"error": "no HIP device visible"}))
@@ -194,23 +333,35 @@ def main():
     info = device_info()
     sync = lambda: call("cxm_device_sync")  # noqa: E731
 
-    if args.workload != "c2":
-        raise SystemExit("only c2 is wired in this build step")
-    launches, desc, keep, x = c2_launches(engine, DeviceArray)
-    total_ms, per = time_launches(launches, args.steps, args.warmup, sync, Event)
-    step_work = sum(l.work for l in launches)
-    value = step_work * args.steps / (total_ms * 1e-3) / 1e9
-    per_op, roof = summarize(launches, total_ms, per, args.steps)
+    if args.copy_calibration:
+        a, b = D((16 << 20,)), D((16 << 20,))
+        for _ in range(3):
+            call("cxm_memcpy_d2d", b.ptr, a.ptr, a.nbytes, None)
+        sync()
+        del a, b
+
+    head = run_workload(args.workload, args.steps, args.warmup, E, D, Event, sync)
     out = {
-        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "metric": METRIC if args.workload != "c5" else "fp32 MLP training step TFLOP/s on 1 MI355X",
+        "value": round(head["value"], 2), "unit": head["unit"], "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(total_ms / args.steps, 5), "higher_is_better": True,
+        "ms_per_step": round(head["ms_per_step"], 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": desc, "frac_of_peak": round(value / PEAK_HBM_GBS, 4),
-        "roofline": roof, "per_op": per_op, "device": info,
+        "config": head["config"], "roofline": head["roofline"], "per_op": head["per_op"],
+        "device": info,
     }
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_c2(x, args.cpu_seconds)
+    if head["unit"] == "GB/s":
+        out["frac_of_peak"] = round(head["value"] / PEAK_HBM_GBS, 4)
+    if not args.no_cpu and args.workload == "c2":
+        out["cpu_baseline"] = cpu_c2(head["host"], args.cpu_seconds)
+    if not args.no_extra:
+        wl = {}
+        for name in [w for w in ["c1", "c3", "c4", "c5"] if w != args.workload]:
+            r = run_workload(name, max(5, args.steps // 5), 2, E, D, Event, sync)
+            wl[name] = {"workload": r["config"]["workload"], "value": round(r["value"], 2),
+                        "unit": r["unit"], "ms_per_step": round(r["ms_per_step"], 5),
+                        "roofline": r["roofline"], "per_op": r["per_op"]}
+        out["workloads"] = wl
     print(json.dumps(out), flush=True)
 
 

@@ -27,17 +27,25 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 // Returns CXM_OK, or the HIP error of the last launch.
 int launch_status();
 
+// Ticket counters sit kCtr words (256 bytes) apart, one per cache line:
+// atomics from many workgroups on counters that share a line serialise
+// (16 counters in one line made a 4096-workgroup reduction 4x slower).
+constexpr size_t kCtr = 64;
+
 // Scratch memory of the multi-pass kernels, one region per (device, stream).
-// The first `counter_words` 32-bit words are tickets, zero on entry to every
-// kernel (each kernel's last workgroup puts its tickets back to zero); the
-// rest is partial results.  Grows on demand (after a stream sync).
+// It starts with `counters` ticket counters (kCtr words each), zero on
+// entry to every kernel (each kernel's last workgroup puts its tickets back
+// to zero); the rest is partial results.  Grows on demand (after a stream
+// sync).  ctr(ws.counters, i) is counter i.
 struct Workspace {
     unsigned *counters;
-    size_t counter_words;
+    size_t counters_n;
     void *scratch;
     size_t scratch_bytes;
 };
-int get_workspace(cxm_stream_t s, size_t counter_words, size_t scratch_bytes, Workspace *ws);
+int get_workspace(cxm_stream_t s, size_t counters, size_t scratch_bytes, Workspace *ws);
+
+__host__ __device__ inline unsigned *ctr(unsigned *base, size_t i) { return base + i * kCtr; }
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -189,6 +197,23 @@ __device__ __forceinline__ ArgPair ld_dev(const ArgPair *p) {
     return {__builtin_bit_cast(float, static_cast<unsigned>(u)), static_cast<int>(u >> 32)};
 }
 
+// Combines n partials p[0], p[stride], ..., p[(n-1)*stride] into `a` in
+// index order.  The device-coherent loads go out 16 at a time so their
+// latencies overlap (one at a time, a 64-partial combine costs ~30 us).
+template <class Op>
+__device__ __forceinline__ typename Op::T combine_partials(const typename Op::T *p, unsigned n,
+                                                           size_t stride, typename Op::T a) {
+    constexpr unsigned G = 16;
+    for (unsigned c0 = 0; c0 < n; c0 += G) {
+        typename Op::T v[G];
+#pragma unroll
+        for (unsigned u = 0; u < G; ++u) v[u] = c0 + u < n ? ld_dev(p + (c0 + u) * stride) : Op::identity();
+#pragma unroll
+        for (unsigned u = 0; u < G; ++u) a = Op::combine(a, v[u]);
+    }
+    return a;
+}
+
 // Last-workgroup ticket.  Every thread of the workgroup calls it after
 // storing its share of the workgroup's partials with st_dev; returns true in
 // all threads of the one workgroup that arrives last among `expected`, which
@@ -206,6 +231,36 @@ __device__ __forceinline__ bool last_block_ticket(unsigned *counter, unsigned ex
         const bool last = (t == expected - 1);
         // ready for the next kernel that uses this workspace
         if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *lds_flag = last ? 1 : 0;
+    }
+    __syncthreads();
+    return *lds_flag != 0;
+}
+
+// Two-level form of the ticket for many arrivals on one output: arrival
+// `idx` (0..expected-1) checks in on group counter idx % G; the last of each
+// group checks in on the top counter counters[G]; the last there is last
+// overall.  Spreads what would be `expected` atomics on one address over
+// G + 1 counters.  `counters` is counter 0 of G + 1 consecutive ones.
+template <unsigned G>
+__device__ __forceinline__ bool last_block_ticket2(unsigned *counters, unsigned expected,
+                                                   unsigned idx, int *lds_flag) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned ng = expected < G ? expected : G;
+        const unsigned g = idx % ng;
+        const unsigned gsize = (expected - g + ng - 1) / ng;
+        bool last = false;
+        const unsigned t =
+            __hip_atomic_fetch_add(ctr(counters, g), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t == gsize - 1) {
+            __hip_atomic_store(ctr(counters, g), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned t2 =
+                __hip_atomic_fetch_add(ctr(counters, G), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = (t2 == ng - 1);
+            if (last) __hip_atomic_store(ctr(counters, G), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         *lds_flag = last ? 1 : 0;
     }
     __syncthreads();

@@ -350,12 +350,9 @@ __global__ __launch_bounds__(kBlock) void k_affine_bwd(const float *__restrict__
     const size_t slot = static_cast<size_t>(tile) * chunks;
     st_dev(&part[((slot + chunk) * 2 + 0) * kAffTile + tid], ms);
     st_dev(&part[((slot + chunk) * 2 + 1) * kAffTile + tid], mb);
-    if (!last_block_ticket(&counters[tile], chunks, &flag)) return;
-    float a = 0.0f, bsum = 0.0f;
-    for (unsigned c = 0; c < chunks; ++c) {
-        a = a + ld_dev(&part[((slot + c) * 2 + 0) * kAffTile + tid]);
-        bsum = bsum + ld_dev(&part[((slot + c) * 2 + 1) * kAffTile + tid]);
-    }
+    if (!last_block_ticket(ctr(counters, tile), chunks, &flag)) return;
+    const float a = combine_partials<SumOp>(part + (slot * 2 + 0) * kAffTile + tid, chunks, 2 * kAffTile, 0.0f);
+    const float bsum = combine_partials<SumOp>(part + (slot * 2 + 1) * kAffTile + tid, chunks, 2 * kAffTile, 0.0f);
     if (col < n) {
         dscale[col] = a;
         dbias[col] = bsum;

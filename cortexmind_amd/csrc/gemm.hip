@@ -232,19 +232,38 @@ __global__ __launch_bounds__(kBlock) void k_gemm(const float *__restrict__ A, co
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) st_dev(&my[out_row(i, r) * BN + out_col(j)], acc[i][j][r]);
-    if (!last_block_ticket(&counters[tile], splits, &flag)) return;
+    if (!last_block_ticket(ctr(counters, tile), splits, &flag)) return;
+    // Sum the splits in split order; each round issues this lane's 64 loads together.
     const float *tp = part + static_cast<size_t>(tile) * splits * (BM * BN);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (unsigned s = 0; s < splits; ++s) {
+        float v[2][2][16];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) v[i][j][r] = ld_dev(&tp[s * (BM * BN) + out_row(i, r) * BN + out_col(j)]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + v[i][j][r];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int lr = out_row(i, r), lc = out_col(j);
-                float v = 0.0f;
-                for (unsigned s = 0; s < splits; ++s) v = v + ld_dev(&tp[s * (BM * BN) + lr * BN + lc]);
-                const size_t row = m0 + lr, col = n0 + lc;
-                if (row < M && col < N) C[row * N + col] = apply_epi(epi, v, row, col, N);
+                const size_t row = m0 + out_row(i, r), col = n0 + out_col(j);
+                if (row < M && col < N) C[row * N + col] = apply_epi(epi, acc[i][j][r], row, col, N);
             }
 }
 

@@ -60,6 +60,8 @@ __device__ __forceinline__ void fold4(typename Op::T (&acc)[4], const float4 v, 
 
 // ------------------------------------------------------------------ rows
 
+constexpr unsigned kTicketGroups = 32;  // per-row ticket counters: 32 groups + 1 top
+
 template <class Op, bool VEC, int UNR>
 __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, size_t dim,
                                                  unsigned segs, size_t seg_len,
@@ -101,9 +103,14 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
         return;
     }
     if (tid == 0) st_dev(&part[row * segs + seg], r);
-    if (!last_block_ticket(&counters[row], segs, &flag)) return;
-    T a = Op::identity();
-    for (unsigned s = tid; s < segs; s += kBlock) a = Op::combine(a, ld_dev(&part[row * segs + s]));
+    // one ticket per row while segments are few, two-level beyond that
+    const bool last = segs <= kTicketGroups
+                          ? last_block_ticket(ctr(counters, row), segs, &flag)
+                          : last_block_ticket2<kTicketGroups>(ctr(counters, row * (kTicketGroups + 1)),
+                                                              segs, seg, &flag);
+    if (!last) return;
+    const unsigned mine = tid < static_cast<int>(segs) ? (segs - tid + kBlock - 1) / kBlock : 0;
+    T a = combine_partials<Op>(part + row * segs + tid, mine, kBlock, Op::identity());
     a = block_reduce<Op, kBlock>(a, lds);
     if (tid == 0) write_out<Op>(out, row, a);
 }
@@ -112,26 +119,39 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
 
 constexpr int kColTile = 256;  // columns per workgroup
 
-template <class Op, bool VEC, int UNR>
-__global__ __launch_bounds__(kBlock) void k_cols(const float *__restrict__ x, size_t dim,
-                                                 size_t inner, unsigned ntiles, unsigned chunks,
-                                                 size_t rows_per_chunk,
-                                                 typename Op::T *__restrict__ part,
-                                                 unsigned *__restrict__ counters, OutDesc out) {
+// NW waves per workgroup.  Vector path: a wave covers the 256 columns with
+// one float4 per lane and wave w takes rows r0+w, r0+w+NW, ...; scalar
+// path: thread t owns column t%256 and rows r0+t/256, step NW/4.  The
+// per-slot results meet in LDS and threads 0..255 combine them in slot
+// order.  Workgroup b -> (tile, chunk, outer slice): with tile_major the
+// chunks of one tile are adjacent in launch order (its combine runs while
+// later tiles still stream), else the tiles of one row chunk are adjacent.
+template <class Op, bool VEC, int UNR, int NW>
+__global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x, size_t dim,
+                                                     size_t inner, unsigned ntiles, unsigned chunks,
+                                                     size_t rows_per_chunk, int tile_major,
+                                                     typename Op::T *__restrict__ part,
+                                                     unsigned *__restrict__ counters, OutDesc out) {
     using T = typename Op::T;
-    __shared__ T lds[kWavesPerBlock][kColTile];
+    constexpr int NSLOT = VEC ? NW : NW / 4;
+    __shared__ T lds[NSLOT][kColTile];
     __shared__ int flag;
 
     const unsigned b = blockIdx.x;
-    const unsigned tile = b % ntiles;
-    const unsigned chunk = (b / ntiles) % chunks;
+    unsigned tile, chunk;
+    if (tile_major) {
+        chunk = b % chunks;
+        tile = (b / chunks) % ntiles;
+    } else {
+        tile = b % ntiles;
+        chunk = (b / ntiles) % chunks;
+    }
     const size_t o = b / (static_cast<size_t>(ntiles) * chunks);
     const int tid = threadIdx.x;
     const float *__restrict__ xo = x + o * dim * inner;
     const size_t r0 = chunk * rows_per_chunk;
     const size_t r1 = r0 + rows_per_chunk < dim ? r0 + rows_per_chunk : dim;
 
-    T mine;  // this thread's column (tile*256 + tid) over the chunk
     if constexpr (VEC) {
         const int lane = tid & (kWave - 1);
         const int w = tid / kWave;
@@ -140,21 +160,20 @@ __global__ __launch_bounds__(kBlock) void k_cols(const float *__restrict__ x, si
         if (col < inner) {
             const float *__restrict__ xc = xo + col;
             size_t r = r0 + w;
-            for (; r + (UNR - 1) * kWavesPerBlock < r1; r += UNR * kWavesPerBlock) {
+            for (; r + (UNR - 1) * NW < r1; r += UNR * NW) {
                 float4 v[UNR];
 #pragma unroll
-                for (int u = 0; u < UNR; ++u)
-                    v[u] = ld4_stream(xc + (r + u * kWavesPerBlock) * inner);
+                for (int u = 0; u < UNR; ++u) v[u] = ld4_stream(xc + (r + u * NW) * inner);
 #pragma unroll
                 for (int u = 0; u < UNR; ++u) {
-                    const int ri = static_cast<int>(r + u * kWavesPerBlock);
+                    const int ri = static_cast<int>(r + u * NW);
                     acc[0] = Op::combine(acc[0], Op::from(v[u].x, ri));
                     acc[1] = Op::combine(acc[1], Op::from(v[u].y, ri));
                     acc[2] = Op::combine(acc[2], Op::from(v[u].z, ri));
                     acc[3] = Op::combine(acc[3], Op::from(v[u].w, ri));
                 }
             }
-            for (; r < r1; r += kWavesPerBlock) {
+            for (; r < r1; r += NW) {
                 const float4 v = ld4_stream(xc + r * inner);
                 const int ri = static_cast<int>(r);
                 acc[0] = Op::combine(acc[0], Op::from(v.x, ri));
@@ -165,28 +184,35 @@ __global__ __launch_bounds__(kBlock) void k_cols(const float *__restrict__ x, si
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) lds[w][lane * 4 + c] = acc[c];
-        __syncthreads();
-        // Wave w held rows r0+w, r0+w+4, ...: combine in wave order.
-        mine = Op::combine(Op::combine(lds[0][tid], lds[1][tid]), Op::combine(lds[2][tid], lds[3][tid]));
     } else {
-        const size_t col = static_cast<size_t>(tile) * kColTile + tid;
-        mine = Op::identity();
+        const int c = tid % kColTile, ph = tid / kColTile;
+        const size_t col = static_cast<size_t>(tile) * kColTile + c;
+        T mine = Op::identity();
         if (col < inner)
-            for (size_t r = r0; r < r1; ++r)
+            for (size_t r = r0 + ph; r < r1; r += NSLOT)
                 mine = Op::combine(mine, Op::from(xo[r * inner + col], static_cast<int>(r)));
+        lds[ph][c] = mine;
     }
-
+    __syncthreads();
+    const bool owner = tid < kColTile;  // threads 0..255 own one column each from here
+    T mine = Op::identity();
+    if (owner) {
+        mine = lds[0][tid];
+#pragma unroll
+        for (int k = 1; k < NSLOT; ++k) mine = Op::combine(mine, lds[k][tid]);
+    }
     const size_t col = static_cast<size_t>(tile) * kColTile + tid;
     if (chunks == 1) {
-        if (col < inner) write_out<Op>(out, o * inner + col, mine);
+        if (owner && col < inner) write_out<Op>(out, o * inner + col, mine);
         return;
     }
     const size_t slot = (o * ntiles + tile) * chunks;
-    st_dev(&part[(slot + chunk) * kColTile + tid], mine);
-    if (!last_block_ticket(&counters[o * ntiles + tile], chunks, &flag)) return;
-    T a = Op::identity();
-    for (unsigned c = 0; c < chunks; ++c) a = Op::combine(a, ld_dev(&part[(slot + c) * kColTile + tid]));
-    if (col < inner) write_out<Op>(out, o * inner + col, a);
+    if (owner) st_dev(&part[(slot + chunk) * kColTile + tid], mine);
+    if (!last_block_ticket(ctr(counters, o * ntiles + tile), chunks, &flag)) return;
+    if (owner) {
+        const T a = combine_partials<Op>(part + slot * kColTile + tid, chunks, kColTile, Op::identity());
+        if (col < inner) write_out<Op>(out, o * inner + col, a);
+    }
 }
 
 __global__ void k_fill_f32(float *z, float v) { *z = v; }
@@ -220,7 +246,8 @@ int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t 
     unsigned *counters = nullptr;
     if (segs > 1) {
         Workspace ws;
-        int rc = get_workspace(s, rows, rows * segs * sizeof(T), &ws);
+        const size_t nctr = segs <= kTicketGroups ? rows : rows * (kTicketGroups + 1);
+        int rc = get_workspace(s, nctr, rows * segs * sizeof(T), &ws);
         if (rc) return rc;
         part = static_cast<T *>(ws.scratch);
         counters = ws.counters;
@@ -239,22 +266,36 @@ int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t 
     return launch_status();
 }
 
+struct ColPlan {
+    int nw;          // waves per workgroup (4 or 16)
+    size_t chunks;   // row chunks per column tile
+    int tile_major;  // launch order
+};
+
+// Default plan: 16-wave workgroups and about one workgroup per CU in
+// total (few chunks, so the last-workgroup combine reads few partials).
+ColPlan col_plan(size_t tiles, size_t dim) {
+    ColPlan p{16, 1, 1};
+    if (tiles < 256) {
+        size_t want = (256 + tiles - 1) / tiles;
+        const size_t max_chunks = (dim + 63) / 64;  // >= 4 rows per wave
+        p.chunks = want < max_chunks ? want : max_chunks;
+        if (p.chunks == 0) p.chunks = 1;
+    }
+    return p;
+}
+
 template <class Op>
-int run_cols(const float *x, size_t outer, size_t dim, size_t inner, OutDesc out, cxm_stream_t s) {
+int run_cols_plan(const float *x, size_t outer, size_t dim, size_t inner, OutDesc out, ColPlan plan,
+                  cxm_stream_t s) {
     using T = typename Op::T;
     hipStream_t hs = reinterpret_cast<hipStream_t>(s);
     const bool vec = aligned16(x) && inner % 4 == 0;
     const size_t ntiles = (inner + kColTile - 1) / kColTile;
     const size_t tiles = ntiles * outer;
-    size_t chunks = 1;
-    if (tiles < kTargetBlocks) {
-        const size_t want = (kTargetBlocks / 2 + tiles - 1) / tiles;
-        const size_t max_chunks = (dim + 15) / 16;  // at least 16 rows (4 per wave) per chunk
-        chunks = want < max_chunks ? want : max_chunks;
-        if (chunks == 0) chunks = 1;
-    }
+    size_t chunks = plan.chunks < 1 ? 1 : plan.chunks;
     size_t rpc = (dim + chunks - 1) / chunks;
-    rpc = (rpc + 3) / 4 * 4;
+    rpc = (rpc + 15) / 16 * 16;
     chunks = (dim + rpc - 1) / rpc;
     if (chunks == 0) chunks = 1;
     const size_t blocks = tiles * chunks;
@@ -270,15 +311,25 @@ int run_cols(const float *x, size_t outer, size_t dim, size_t inner, OutDesc out
         counters = ws.counters;
     }
     const unsigned nb = static_cast<unsigned>(blocks);
-    if (vec)
-        hipLaunchKernelGGL((k_cols<Op, true, 8>), dim3(nb), dim3(kBlock), 0, hs, x, dim, inner,
-                           static_cast<unsigned>(ntiles), static_cast<unsigned>(chunks), rpc, part,
-                           counters, out);
-    else
-        hipLaunchKernelGGL((k_cols<Op, false, 1>), dim3(nb), dim3(kBlock), 0, hs, x, dim, inner,
-                           static_cast<unsigned>(ntiles), static_cast<unsigned>(chunks), rpc, part,
-                           counters, out);
+    const unsigned nt = static_cast<unsigned>(ntiles), nc = static_cast<unsigned>(chunks);
+#define CXM_COLS(VEC_, UNR_, NW_)                                                                   \
+    hipLaunchKernelGGL((k_cols<Op, VEC_, UNR_, NW_>), dim3(nb), dim3(NW_ * kWave), 0, hs, x, dim, inner, \
+                       nt, nc, rpc, plan.tile_major, part, counters, out)
+    if (plan.nw == 16) {
+        if (vec) CXM_COLS(true, 8, 16);
+        else CXM_COLS(false, 1, 16);
+    } else {
+        if (vec) CXM_COLS(true, 8, 4);
+        else CXM_COLS(false, 1, 4);
+    }
+#undef CXM_COLS
     return launch_status();
+}
+
+template <class Op>
+int run_cols(const float *x, size_t outer, size_t dim, size_t inner, OutDesc out, cxm_stream_t s) {
+    const size_t tiles = (inner + kColTile - 1) / kColTile * outer;
+    return run_cols_plan<Op>(x, outer, dim, inner, out, col_plan(tiles, dim), s);
 }
 
 enum Which { kSum, kMean, kMax, kArgMax };

@@ -23,7 +23,7 @@ int st(hipError_t e) { return e == hipSuccess ? CXM_OK : static_cast<int>(e); }
 
 struct WsEntry {
     void *base = nullptr;
-    size_t counter_words = 0;
+    size_t counters = 0;
     size_t scratch_bytes = 0;
 };
 
@@ -36,18 +36,18 @@ namespace cxm {
 
 int launch_status() { return st(hipGetLastError()); }
 
-int get_workspace(cxm_stream_t s, size_t counter_words, size_t scratch_bytes, Workspace *ws) {
+int get_workspace(cxm_stream_t s, size_t counters, size_t scratch_bytes, Workspace *ws) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return st(e);
     std::lock_guard<std::mutex> lk(g_ws_mu);
     WsEntry &w = g_ws[{dev, s}];
-    if (w.base == nullptr || w.counter_words < counter_words || w.scratch_bytes < scratch_bytes) {
-        size_t cw = counter_words < 16384 ? 16384 : counter_words;
+    if (w.base == nullptr || w.counters < counters || w.scratch_bytes < scratch_bytes) {
+        size_t nc = counters < 1024 ? 1024 : counters;
         size_t sb = scratch_bytes < (size_t(8) << 20) ? (size_t(8) << 20) : scratch_bytes;
-        if (w.counter_words > cw) cw = w.counter_words;
+        if (w.counters > nc) nc = w.counters;
         if (w.scratch_bytes > sb) sb = w.scratch_bytes;
-        cw = (cw + 63) & ~size_t(63);  // keep the scratch 256-byte aligned
+        const size_t cw = nc * cxm::kCtr;  // words; a multiple of 64 keeps the scratch 256-byte aligned
         if (w.base != nullptr) {
             // Kernels queued on this stream may still use the old region.
             e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(s));
@@ -65,12 +65,12 @@ int get_workspace(cxm_stream_t s, size_t counter_words, size_t scratch_bytes, Wo
             return st(e);
         }
         w.base = p;
-        w.counter_words = cw;
+        w.counters = nc;
         w.scratch_bytes = sb;
     }
     ws->counters = static_cast<unsigned *>(w.base);
-    ws->counter_words = w.counter_words;
-    ws->scratch = static_cast<unsigned *>(w.base) + w.counter_words;
+    ws->counters_n = w.counters;
+    ws->scratch = static_cast<unsigned *>(w.base) + w.counters * cxm::kCtr;
     ws->scratch_bytes = w.scratch_bytes;
     return CXM_OK;
 }

@@ -350,8 +350,8 @@ __global__ __launch_bounds__(kBlock) void k_xent(const float *__restrict__ logit
     }
     if (threadIdx.x == 0) st_dev(&part[blockIdx.x], nll);
     if (!last_block_ticket(counter, gridDim.x, &flag)) return;
-    float t = 0.0f;
-    for (unsigned i = threadIdx.x; i < gridDim.x; i += kBlock) t += ld_dev(&part[i]);
+    const unsigned mine = threadIdx.x < gridDim.x ? (gridDim.x - threadIdx.x + kBlock - 1) / kBlock : 0;
+    float t = combine_partials<SumOp>(part + threadIdx.x, mine, kBlock, 0.0f);
     t = block_reduce<SumOp, kBlock>(t, lds);
     if (threadIdx.x == 0) loss[0] = t / static_cast<float>(b);
 }
