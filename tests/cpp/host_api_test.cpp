@@ -1,0 +1,108 @@
+// Drives the backend through the C++ host layer (include/cortex_hip.hpp),
+// the way a C++ caller of the reference engine would: device buffers from
+// cxm_dev_malloc, operators named as in Engine/AVX2, results copied back
+// and checked against values computed here.  Inputs are small integers, so
+// every sum is exact whatever the summation order.  Prints "ALL OK" and
+// returns 0 when every check passes; a failed check prints what differed
+// and returns 1; a failed call exits(1) inside the host layer.
+#include <cmath>
+#include <cstdio>
+#include <vector>
+
+#include "cortex_hip.hpp"
+
+namespace hip = cortex::_fw::hip;
+
+template <class T>
+struct Dev {
+    T *p = nullptr;
+    size_t n;
+    explicit Dev(size_t n_) : n(n_) { hip::check(cxm_dev_malloc(reinterpret_cast<void **>(&p), n * sizeof(T)), "malloc"); }
+    Dev(const std::vector<T> &h) : Dev(h.size()) { hip::check(cxm_memcpy_h2d(p, h.data(), n * sizeof(T), nullptr), "h2d"); }
+    std::vector<T> get() const {
+        std::vector<T> h(n);
+        hip::check(cxm_memcpy_d2h(h.data(), p, n * sizeof(T), nullptr), "d2h");
+        return h;
+    }
+    ~Dev() { cxm_dev_free(p); }
+};
+
+static int failures = 0;
+#define EXPECT(cond, ...)                     \
+    do {                                      \
+        if (!(cond)) {                        \
+            std::printf("FAIL: " __VA_ARGS__); \
+            std::printf("\n");                \
+            ++failures;                       \
+        }                                     \
+    } while (0)
+
+int main() {
+    int n = 0;
+    if (cxm_device_count(&n) != CXM_OK || n < 1) {
+        std::printf("no device\n");
+        return 2;
+    }
+    const size_t R = 300, C = 1028;
+    std::vector<float> x(R * C);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = static_cast<float>(static_cast<int>((i * 2654435761u) % 201) - 100);
+    x[5 * C + 77] = 1000.0f;  // row 5 maximum at column 77
+    x[9 * C + 3] = 1000.0f;   // column 3 maximum at row 9
+    Dev<float> dx(x);
+
+    // reduce::sum / max / argmax, row and column forms
+    Dev<float> zr(R), zc(C);
+    Dev<int32_t> ar(R), ac(C);
+    hip::reduce::sum(dx.p, zr.p, R, C, 1);
+    hip::reduce::sum(dx.p, zc.p, 1, R, C);
+    hip::reduce::argmax(dx.p, ar.p, R, C, 1);
+    hip::reduce::argmax(dx.p, ac.p, 1, R, C);
+    auto hr = zr.get(), hc = zc.get();
+    auto har = ar.get(), hac = ac.get();
+    for (size_t r = 0; r < R; ++r) {
+        double s = 0;
+        for (size_t c = 0; c < C; ++c) s += x[r * C + c];
+        EXPECT(hr[r] == static_cast<float>(s), "row sum %zu: %f vs %f", r, hr[r], s);
+    }
+    for (size_t c = 0; c < C; ++c) {
+        double s = 0;
+        for (size_t r = 0; r < R; ++r) s += x[r * C + c];
+        EXPECT(hc[c] == static_cast<float>(s), "col sum %zu", c);
+    }
+    EXPECT(har[5] == 77, "row argmax 5 = %d", har[5]);
+    EXPECT(hac[3] == 9, "col argmax 3 = %d", hac[3]);
+    Dev<float> g(1);
+    hip::reduce::max(dx.p, g.p, R * C);
+    EXPECT(g.get()[0] == 1000.0f, "global max");
+
+    // Broadcast::row::add in place, then matrix_t::mul and activation::relu
+    std::vector<float> b(C);
+    for (size_t c = 0; c < C; ++c) b[c] = static_cast<float>(c % 7) - 3.0f;
+    Dev<float> db(b), dy(R * C);
+    hip::Broadcast::row::add(dx.p, db.p, R, C);
+    hip::activation::relu(dx.p, dy.p, R * C);
+    auto hy = dy.get();
+    for (size_t i = 0; i < hy.size(); ++i) {
+        const float t = x[i] + b[i % C];
+        EXPECT(hy[i] == (0.0f > t ? 0.0f : t), "relu(x+b) at %zu", i);
+        if (failures > 10) break;
+    }
+
+    // matrix_t::matmul on small integers (exact in fp32)
+    const size_t M = 70, K = 33, N = 45;
+    std::vector<float> A(M * K), B(K * N);
+    for (size_t i = 0; i < A.size(); ++i) A[i] = static_cast<float>(static_cast<int>(i % 9) - 4);
+    for (size_t i = 0; i < B.size(); ++i) B[i] = static_cast<float>(static_cast<int>(i % 5) - 2);
+    Dev<float> dA(A), dB(B), dC(M * N);
+    hip::matrix_t::matmul(dA.p, dB.p, dC.p, M, K, N);
+    auto hC = dC.get();
+    for (size_t i = 0; i < M; ++i)
+        for (size_t j = 0; j < N; ++j) {
+            float s = 0;
+            for (size_t k = 0; k < K; ++k) s += A[i * K + k] * B[k * N + j];
+            EXPECT(hC[i * N + j] == s, "matmul %zu,%zu", i, j);
+        }
+
+    if (failures == 0) std::printf("ALL OK\n");
+    return failures == 0 ? 0 : 1;
+}

@@ -79,3 +79,16 @@ def test_empty_outputs_are_noops():
     assert lib.cxm_binary_f32(p, p, p, 0, 0, None) == 0
     assert lib.cxm_softmax_fwd_f32(p, p, 0, 8, 0, None) == 0
     assert lib.cxm_gemm_f32(p, p, p, 0, 4, 4, 0, 0, None, 0, None, None) == 0
+
+
+def test_cpp_host_layer_builds_and_links():
+    """The C++ mirror header compiles with a plain host compiler and the
+    test program links against the library (run on the GPU elsewhere)."""
+    import os
+    import subprocess
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = subprocess.run(["make", "-s", "-C", os.path.join(root, "tests", "cpp")], capture_output=True,
+                         text=True)
+    assert out.returncode == 0, out.stderr
+    assert os.path.exists(os.path.join(root, "tests", "cpp", "host_api_test"))
