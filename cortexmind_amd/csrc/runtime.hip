@@ -178,7 +178,7 @@ int cxm_stream_destroy(cxm_stream_t s) {
         for (auto it = g_ws.begin(); it != g_ws.end();) {
             if (it->first.second == s) {
                 (void)hipStreamSynchronize(reinterpret_cast<hipStream_t>(s));
-                (void)hipFree(it->second.base);
+                if (it->second.base) (void)hipFree(it->second.base);
                 it = g_ws.erase(it);
             } else {
                 ++it;
@@ -225,7 +225,7 @@ int cxm_release_workspaces(void) {
     for (auto &kv : g_ws) {
         (void)hipSetDevice(kv.first.first);
         hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(kv.first.second));
-        if (e == hipSuccess) e = hipFree(kv.second.base);
+        if (e == hipSuccess && kv.second.base) e = hipFree(kv.second.base);
         if (e != hipSuccess && rc == CXM_OK) rc = st(e);
     }
     g_ws.clear();
