@@ -47,7 +47,23 @@ int get_workspace(cxm_stream_t s, size_t counters, size_t scratch_bytes, Workspa
 
 __host__ __device__ inline unsigned *ctr(unsigned *base, size_t i) { return base + i * kCtr; }
 
-inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// Epilogue of the GEMM (gemm.hip), applied to each finished sum
+// v = (op(A) op(B))[row, col] before it is stored in C (row-major [M, N]).
+struct Epilogue {
+    const float *bias;  // [N] or null: v + bias[col]
+    const float *gate;  // [M, N] or null: v * (gate > 0 ? 1 : 0) (ReLU backward)
+    int act;            // CXM_ACT_NONE or CXM_ACT_RELU
+    int sgd;            // 1: C is a weight and gets C - v*lr (SGD fused on the gradient)
+    float lr;
+};
+// C[M, N] = op(A) op(B) with the epilogue; the engine of cxm_gemm_f32.
+int gemm_ex(const float *A, const float *B, float *C, size_t M, size_t K, size_t N, int ta, int tb,
+            const Epilogue &epi, cxm_stream_t s);
+// b[j] = b[j] - lr * sum_i x[i, j] over x [rows, cols]: a bias gradient
+// (reduce::sum over axis 0) and its SGD step in one pass (reduce.hip).
+int colsum_sgd(const float *x, float *b, size_t rows, size_t cols, float lr, cxm_stream_t s);
+
+__host__ __device__ inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline unsigned ceil_div(size_t a, size_t b) { return static_cast<unsigned>((a + b - 1) / b); }
 

@@ -6,9 +6,9 @@
 // (Engine/CUDA/matrix.cu:112-159, cuBLAS with TF32 compute).  This kernel is
 // true fp32: every product and sum is an fp32 operation of the MFMA unit.
 //
-// Tiling: a 256-thread workgroup computes a 128x128 tile of C; its four
-// waves each own 64x64 = 2x2 MFMA tiles of 32x32 (64 accumulator
-// registers per lane).  K advances in steps of 16 through double-buffered
+// Tiling: a 512-thread workgroup computes a 128x128 tile of C; its eight
+// waves (two per SIMD, so one hides the other's LDS and barrier waits) each
+// own 64x32 = 2x1 MFMA tiles of 32x32 (32 accumulator registers per lane).  K advances in steps of 32 through double-buffered
 // LDS tiles stored k-major (As[k][m], Bs[k][n]), so every fragment read is
 // one ds_read_b32 with consecutive lanes on consecutive addresses whatever
 // the global layout; global->LDS loads are 128-bit when the leading
@@ -27,22 +27,29 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 16, PAD = 4;
+constexpr int BM = 128, BN = 128, BK = 32, PAD = 4;
+constexpr int KQ = BK / 4;                      // 4-element groups along k in a tile row
+constexpr int kGemmThreads = 512;               // 8 waves: 2 (m) x 4 (n), each 64 x 32 of C
+constexpr int WI = 2, WJ = 1;                   // 32x32 MFMA tiles per wave along m and n
+constexpr int SLOTS = BM * BK / 4 / kGemmThreads;  // float4 groups per thread per tile (A and B alike)
+constexpr int kColTileThin = 256;  // m columns per workgroup of the thin TN kernel
 
-struct Epilogue {
-    const float *bias;  // [N] or null
-    const float *gate;  // [M, N] or null: multiply by (gate > 0 ? 1 : 0)
-    int act;            // CXM_ACT_NONE or CXM_ACT_RELU
-};
 
-__device__ __forceinline__ float apply_epi(const Epilogue &e, float v, size_t row, size_t col, size_t N) {
+__device__ __forceinline__ void store_epi(const Epilogue &e, float *C, size_t row, size_t col, size_t N,
+                                          float v) {
+    float *p = C + row * N + col;
+    if (e.sgd) {
+        const float t = v * e.lr;  // matrix_t::sub(W, ScalarOp::mul(G, lr)): two roundings
+        *p = *p - t;
+        return;
+    }
     if (e.bias) v = v + e.bias[col];
     if (e.act == CXM_ACT_RELU) v = 0.0f > v ? 0.0f : v;
     if (e.gate) v = v * (e.gate[row * N + col] > 0.0f ? 1.0f : 0.0f);
-    return v;
+    *p = v;
 }
 
-// Loads one 4-element group of the A tile (slot 0..511) into registers.
+// Loads one 4-element group of the A tile (slot 0..BM*BK/4-1) into registers.
 // Non-transposed A [M,K]: group = 4 consecutive k of one row.
 // Transposed A (stored [K,M]): group = 4 consecutive m of one k.
 template <bool TA, bool VA>
@@ -51,13 +58,13 @@ __device__ __forceinline__ float4 load_a(const float *__restrict__ A, int slot, 
     size_t r, c;  // index in the stored matrix of the group's first element
     size_t lim_r, lim_c;
     if constexpr (!TA) {
-        r = m0 + slot / 4;
-        c = k0 + (slot % 4) * 4;
+        r = m0 + slot / KQ;
+        c = k0 + (slot % KQ) * 4;
         lim_r = M;
         lim_c = K;
     } else {
-        r = k0 + slot / 32;
-        c = m0 + (slot % 32) * 4;
+        r = k0 + slot / (BM / 4);
+        c = m0 + (slot % (BM / 4)) * 4;
         lim_r = K;
         lim_c = M;
     }
@@ -79,13 +86,13 @@ __device__ __forceinline__ float4 load_b(const float *__restrict__ B, int slot, 
                                          size_t N, size_t K) {
     size_t r, c, lim_r, lim_c;
     if constexpr (!TB) {
-        r = k0 + slot / 32;
-        c = n0 + (slot % 32) * 4;
+        r = k0 + slot / (BN / 4);
+        c = n0 + (slot % (BN / 4)) * 4;
         lim_r = K;
         lim_c = N;
     } else {
-        r = n0 + slot / 4;
-        c = k0 + (slot % 4) * 4;
+        r = n0 + slot / KQ;
+        c = k0 + (slot % KQ) * 4;
         lim_r = N;
         lim_c = K;
     }
@@ -103,13 +110,13 @@ __device__ __forceinline__ float4 load_b(const float *__restrict__ B, int slot, 
 template <bool TA>
 __device__ __forceinline__ void store_a(float (*As)[BM + PAD], int slot, float4 v) {
     if constexpr (!TA) {
-        const int m = slot / 4, k = (slot % 4) * 4;
+        const int m = slot / KQ, k = (slot % KQ) * 4;
         As[k + 0][m] = v.x;
         As[k + 1][m] = v.y;
         As[k + 2][m] = v.z;
         As[k + 3][m] = v.w;
     } else {
-        const int k = slot / 32, m = (slot % 32) * 4;
+        const int k = slot / (BM / 4), m = (slot % (BM / 4)) * 4;
         *reinterpret_cast<float4 *>(&As[k][m]) = v;
     }
 }
@@ -117,10 +124,10 @@ __device__ __forceinline__ void store_a(float (*As)[BM + PAD], int slot, float4 
 template <bool TB>
 __device__ __forceinline__ void store_b(float (*Bs)[BN + PAD], int slot, float4 v) {
     if constexpr (!TB) {
-        const int k = slot / 32, n = (slot % 32) * 4;
+        const int k = slot / (BN / 4), n = (slot % (BN / 4)) * 4;
         *reinterpret_cast<float4 *>(&Bs[k][n]) = v;
     } else {
-        const int n = slot / 4, k = (slot % 4) * 4;
+        const int n = slot / KQ, k = (slot % KQ) * 4;
         Bs[k + 0][n] = v.x;
         Bs[k + 1][n] = v.y;
         Bs[k + 2][n] = v.z;
@@ -129,7 +136,7 @@ __device__ __forceinline__ void store_b(float (*Bs)[BN + PAD], int slot, float4 
 }
 
 template <bool TA, bool TB, bool VA, bool VB>
-__global__ __launch_bounds__(kBlock) void k_gemm(const float *__restrict__ A, const float *__restrict__ B,
+__global__ __launch_bounds__(kGemmThreads) void k_gemm(const float *__restrict__ A, const float *__restrict__ B,
                                                  float *__restrict__ C, size_t M, size_t N, size_t K,
                                                  unsigned tiles_n, unsigned splits, size_t kper,
                                                  Epilogue epi, float *__restrict__ part,
@@ -148,29 +155,29 @@ __global__ __launch_bounds__(kBlock) void k_gemm(const float *__restrict__ A, co
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave >> 2, wn = wave & 3;
     const int l32 = lane & 31, lhi = lane >> 5;
 
-    floatx16 acc[2][2];
+    floatx16 acc[WI][WJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    float4 ra[2], rb[2];
+    float4 ra[SLOTS], rb[SLOTS];
     int buf = 0;
     if (kbeg < kend) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            ra[s] = load_a<TA, VA>(A, tid + s * kBlock, m0, kbeg, M, K);
-            rb[s] = load_b<TB, VB>(B, tid + s * kBlock, n0, kbeg, N, K);
+        for (int s = 0; s < SLOTS; ++s) {
+            ra[s] = load_a<TA, VA>(A, tid + s * kGemmThreads, m0, kbeg, M, K);
+            rb[s] = load_b<TB, VB>(B, tid + s * kGemmThreads, n0, kbeg, N, K);
         }
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            store_a<TA>(As[0], tid + s * kBlock, ra[s]);
-            store_b<TB>(Bs[0], tid + s * kBlock, rb[s]);
+        for (int s = 0; s < SLOTS; ++s) {
+            store_a<TA>(As[0], tid + s * kGemmThreads, ra[s]);
+            store_b<TB>(Bs[0], tid + s * kGemmThreads, rb[s]);
         }
     }
     __syncthreads();
@@ -179,29 +186,53 @@ __global__ __launch_bounds__(kBlock) void k_gemm(const float *__restrict__ A, co
         const bool more = k0 + BK < kend;
         if (more) {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                ra[s] = load_a<TA, VA>(A, tid + s * kBlock, m0, k0 + BK, M, K);
-                rb[s] = load_b<TB, VB>(B, tid + s * kBlock, n0, k0 + BK, N, K);
+            for (int s = 0; s < SLOTS; ++s) {
+                ra[s] = load_a<TA, VA>(A, tid + s * kGemmThreads, m0, k0 + BK, M, K);
+                rb[s] = load_b<TB, VB>(B, tid + s * kGemmThreads, n0, k0 + BK, N, K);
             }
         }
+        // Software-pipelined over k-steps of 2: the fragments of step t+1 are
+        // read from LDS before the four MFMAs of step t are issued, so the
+        // LDS latency hides behind 256 cycles of matrix work instead of
+        // leaving the MFMA pipe idle once per step.
+        float ca[WI], cb[WJ];
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += 2) {
-            float a[2], b[2];
+        for (int i = 0; i < WI; ++i) ca[i] = As[buf][lhi][wm * 64 + i * 32 + l32];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) a[i] = As[buf][kk + lhi][wm * 64 + i * 32 + l32];
+        for (int j = 0; j < WJ; ++j) cb[j] = Bs[buf][lhi][wn * 32 + j * 32 + l32];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) b[j] = Bs[buf][kk + lhi][wn * 64 + j * 32 + l32];
+        for (int t = 0; t < BK / 2; ++t) {
+            float na[WI], nb[WJ];
+            if (t + 1 < BK / 2) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+                for (int i = 0; i < WI; ++i) na[i] = As[buf][2 * (t + 1) + lhi][wm * 64 + i * 32 + l32];
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < WJ; ++j) nb[j] = Bs[buf][2 * (t + 1) + lhi][wn * 32 + j * 32 + l32];
+            }
+#pragma unroll
+            for (int i = 0; i < WI; ++i)
+#pragma unroll
+                for (int j = 0; j < WJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[i], cb[j], acc[i][j], 0, 0, 0);
+            if (t + 1 < BK / 2) {
+#pragma unroll
+                for (int i = 0; i < WI; ++i) ca[i] = na[i];
+#pragma unroll
+                for (int j = 0; j < WJ; ++j) cb[j] = nb[j];
+            }
+        }
+        // Scheduling groups: reads of step 0, then (reads of step t+1, MFMAs of step t).
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+        for (int t = 0; t < BK / 2; ++t) {
+            if (t + 1 < BK / 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, WI * WJ, 0);
         }
         if (more) {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                store_a<TA>(As[buf ^ 1], tid + s * kBlock, ra[s]);
-                store_b<TB>(Bs[buf ^ 1], tid + s * kBlock, rb[s]);
+            for (int s = 0; s < SLOTS; ++s) {
+                store_a<TA>(As[buf ^ 1], tid + s * kGemmThreads, ra[s]);
+                store_b<TB>(Bs[buf ^ 1], tid + s * kGemmThreads, rb[s]);
             }
         }
         __syncthreads();
@@ -210,61 +241,269 @@ __global__ __launch_bounds__(kBlock) void k_gemm(const float *__restrict__ A, co
 
     // Output element of accumulator (i, j, r) for this lane.
     auto out_row = [&](int i, int r) { return wm * 64 + i * 32 + 8 * (r / 4) + 4 * lhi + (r % 4); };
-    auto out_col = [&](int j) { return wn * 64 + j * 32 + l32; };
+    auto out_col = [&](int j) { return wn * 32 + j * 32 + l32; };
 
     if (splits == 1) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < WI; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < WJ; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const size_t row = m0 + out_row(i, r), col = n0 + out_col(j);
-                    if (row < M && col < N) C[row * N + col] = apply_epi(epi, acc[i][j][r], row, col, N);
+                    if (row < M && col < N) store_epi(epi, C, row, col, N, acc[i][j][r]);
                 }
         return;
     }
 
     float *my = part + (static_cast<size_t>(tile) * splits + split) * (BM * BN);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) st_dev(&my[out_row(i, r) * BN + out_col(j)], acc[i][j][r]);
     if (!last_block_ticket(ctr(counters, tile), splits, &flag)) return;
     // Sum the splits in split order; each round issues this lane's 64 loads together.
     const float *tp = part + static_cast<size_t>(tile) * splits * (BM * BN);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     for (unsigned s = 0; s < splits; ++s) {
-        float v[2][2][16];
+        float v[WI][WJ][16];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < WI; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < WJ; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) v[i][j][r] = ld_dev(&tp[s * (BM * BN) + out_row(i, r) * BN + out_col(j)]);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < WI; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < WJ; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + v[i][j][r];
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const size_t row = m0 + out_row(i, r), col = n0 + out_col(j);
-                if (row < M && col < N) C[row * N + col] = apply_epi(epi, acc[i][j][r], row, col, N);
+                if (row < M && col < N) store_epi(epi, C, row, col, N, acc[i][j][r]);
             }
+}
+
+// ------------------------------------------------ skinny products
+// Products with a dimension of at most 16 (the 10-class output layer of
+// the MLP) leave a 128x128 MFMA tile almost empty; they are bandwidth
+// work and get their own kernels (plain fp32 fma, fixed order per lane,
+// then a fixed tree).
+
+constexpr int kThin = 16;
+
+// NN with N <= 16 and K <= 1024: B^T is staged once per workgroup in LDS
+// (Bs[n][k], zero rows for n >= N); a 1024-thread workgroup computes 16
+// rows of C, one per wave, lane l taking k = 4l..4l+3 (+256 per step) with
+// 128-bit loads of A, then a wave reduction per output column.
+constexpr int kThinNT = 1024;
+
+__global__ __launch_bounds__(kThinNT) void k_gemm_thin_n(const float *__restrict__ A, const float *__restrict__ B,
+                                                        float *__restrict__ C, size_t M, size_t N, size_t K,
+                                                        Epilogue epi) {
+    extern __shared__ float Bs[];  // [kThin][K]; K <= 1024: one k per thread
+    {
+        const size_t k = threadIdx.x;
+        float t[kThin];  // all loads issued before any store
+#pragma unroll
+        for (int n = 0; n < kThin; ++n) t[n] = (k < K && n < static_cast<int>(N)) ? B[k * N + n] : 0.0f;
+        if (k < K)
+#pragma unroll
+            for (int n = 0; n < kThin; ++n) Bs[n * K + k] = t[n];
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const size_t i = static_cast<size_t>(blockIdx.x) * (kThinNT / kWave) + w;
+    if (i >= M) return;  // whole wave; no barrier follows
+    const size_t k4n = K / 4;
+    float acc[kThin];
+#pragma unroll
+    for (int n = 0; n < kThin; ++n) acc[n] = 0.0f;
+    for (size_t k4 = lane; k4 < k4n; k4 += 4 * kWave) {
+        float4 a[4];  // four 128-bit loads of A in flight
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            a[u] = k4 + u * kWave < k4n ? ld4(A + i * K + 4 * (k4 + u * kWave)) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (k4 + u * kWave >= k4n) break;
+#pragma unroll
+            for (int n = 0; n < kThin; ++n) {
+                const float4 b = *reinterpret_cast<const float4 *>(&Bs[n * K + 4 * (k4 + u * kWave)]);
+                acc[n] = __builtin_fmaf(a[u].w, b.w, __builtin_fmaf(a[u].z, b.z, __builtin_fmaf(a[u].y, b.y, __builtin_fmaf(a[u].x, b.x, acc[n]))));
+            }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < kThin; ++n) acc[n] = wave_reduce<SumOp>(acc[n]);
+    if (lane < static_cast<int>(N)) {
+        float v = 0.0f;
+#pragma unroll
+        for (int n = 0; n < kThin; ++n) v = lane == n ? acc[n] : v;
+        store_epi(epi, C, i, lane, N, v);
+    }
+}
+
+// TN with N <= 16: C[m, n] = sum_k A[k, m] * B[k, n], A stored [K, M]
+// (M % 4 == 0), B stored [K, N].  Pass 1: a workgroup takes 256 columns of
+// m (float4 per lane) and a chunk of k; its 4 waves take interleaved k and
+// meet in LDS; the chunk's sums go to the workspace.  Pass 2: one thread
+// per output adds the chunks in order and applies the epilogue.  (A
+// last-workgroup combine here would make one workgroup read all
+// chunks x 256 x N partials, tens of microseconds of serial latency.)
+__global__ __launch_bounds__(kBlock) void k_gemm_thin_tn(const float *__restrict__ A, const float *__restrict__ B,
+                                                        size_t M, size_t N, size_t K, unsigned ntiles, size_t kpc,
+                                                        float *__restrict__ part) {
+    __shared__ float lds[kWavesPerBlock][kThin][kColTileThin];
+    const unsigned tile = blockIdx.x % ntiles, chunk = blockIdx.x / ntiles;
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave, tid = threadIdx.x;
+    const size_t m = static_cast<size_t>(tile) * kColTileThin + lane * 4;
+    const size_t k0 = static_cast<size_t>(chunk) * kpc, k1 = k0 + kpc < K ? k0 + kpc : K;
+    float acc[4][kThin];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int n = 0; n < kThin; ++n) acc[c][n] = 0.0f;
+    if (m < M) {
+        constexpr int U = 4;  // rows of loads in flight per wave
+        for (size_t k = k0 + w; k < k1; k += U * kWavesPerBlock) {
+            float4 a[U];
+            float b[U][kThin];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const size_t kk = k + u * kWavesPerBlock;
+                const bool in = kk < k1;
+                a[u] = in ? ld4(A + kk * M + m) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int n = 0; n < kThin; ++n) b[u][n] = (in && n < static_cast<int>(N)) ? B[kk * N + n] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int n = 0; n < kThin; ++n) {
+                    acc[0][n] = __builtin_fmaf(a[u].x, b[u][n], acc[0][n]);
+                    acc[1][n] = __builtin_fmaf(a[u].y, b[u][n], acc[1][n]);
+                    acc[2][n] = __builtin_fmaf(a[u].z, b[u][n], acc[2][n]);
+                    acc[3][n] = __builtin_fmaf(a[u].w, b[u][n], acc[3][n]);
+                }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int n = 0; n < kThin; ++n) lds[w][n][lane * 4 + c] = acc[c][n];
+    __syncthreads();
+    // part[chunk][n][m]: column tile*256 + tid, waves combined in order
+    float *dst = part + static_cast<size_t>(chunk) * kThin * M + static_cast<size_t>(tile) * kColTileThin + tid;
+    if (static_cast<size_t>(tile) * kColTileThin + tid < M)
+#pragma unroll
+        for (int n = 0; n < kThin; ++n)
+            dst[static_cast<size_t>(n) * M] = (lds[0][n][tid] + lds[1][n][tid]) + (lds[2][n][tid] + lds[3][n][tid]);
+}
+
+__global__ __launch_bounds__(kBlock) void k_gemm_thin_tn_sum(const float *__restrict__ part, float *__restrict__ C,
+                                                            size_t M, size_t N, unsigned chunks, Epilogue epi) {
+    const size_t q = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;  // q = n * M + m
+    if (q >= N * M) return;
+    const size_t n = q / M, m = q - n * M;
+    float v = 0.0f;
+    unsigned c = 0;
+    for (; c + 16 <= chunks; c += 16) {
+        float t[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) t[u] = part[(static_cast<size_t>(c + u) * kThin + n) * M + m];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v = v + t[u];
+    }
+    for (; c < chunks; ++c) v = v + part[(static_cast<size_t>(c) * kThin + n) * M + m];
+    store_epi(epi, C, m, n, N, v);
+}
+
+// Small K (<= 16), A [M, K] row-major: every output is a K-term dot
+// product, so this streams C (and the gate).  The workgroup's K x 1024
+// panel of B is staged in LDS once; thread t keeps the K x 4 fragment of
+// columns j0 + 4*(t % 256) in registers and takes rows r0 + t/256 + 4i of
+// the workgroup's 16, all four rows' loads issued together.
+constexpr int kThinCols = 1024;
+constexpr int kThinRows = 16;
+
+template <bool TB>
+__global__ __launch_bounds__(kThinNT) void k_gemm_thin_k(const float *__restrict__ A, const float *__restrict__ B,
+                                                        float *__restrict__ C, size_t M, size_t N, size_t K,
+                                                        Epilogue epi) {
+    __shared__ float Bs[kThin][kThinCols];
+    const size_t j0 = static_cast<size_t>(blockIdx.x) * kThinCols;
+    {
+        const size_t j = j0 + threadIdx.x;
+        float t[kThin];  // all loads issued before any store
+#pragma unroll
+        for (int k = 0; k < kThin; ++k)
+            t[k] = (k < static_cast<int>(K) && j < N) ? (TB ? B[j * K + k] : B[k * N + j]) : 0.0f;
+#pragma unroll
+        for (int k = 0; k < kThin; ++k) Bs[k][threadIdx.x] = t[k];
+    }
+    __syncthreads();
+    const int ct = threadIdx.x % 256, rg = threadIdx.x / 256;
+    const size_t j = j0 + 4 * ct;
+    if (j >= N) return;  // no barrier follows
+    float bf[kThin][4];
+#pragma unroll
+    for (int k = 0; k < kThin; ++k)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) bf[k][c] = Bs[k][4 * ct + c];
+    const bool vec = j + 3 < N && !epi.sgd && !epi.bias && aligned16(C) && N % 4 == 0 &&
+                     (!epi.gate || aligned16(epi.gate));
+    const size_t r0 = static_cast<size_t>(blockIdx.y) * kThinRows + rg;
+    float4 g[4];  // the four rows' gate loads go out together
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const size_t r = r0 + 4 * i;
+        g[i] = (vec && epi.gate && r < M) ? ld4(epi.gate + r * N + j) : make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // the row index is the same in the whole wave: keep A's row in scalar registers
+        const int r = __builtin_amdgcn_readfirstlane(static_cast<int>(r0 + 4 * i));
+        if (static_cast<size_t>(r) >= M) break;
+        const float *__restrict__ ar = A + static_cast<size_t>(r) * K;
+        float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < kThin; ++k) {
+            const float a = k < static_cast<int>(K) ? ar[k] : 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o[c] = __builtin_fmaf(a, bf[k][c], o[c]);
+        }
+        if (vec) {
+            float4 v = make_float4(o[0], o[1], o[2], o[3]);
+            if (epi.act == CXM_ACT_RELU) {
+                v.x = 0.0f > v.x ? 0.0f : v.x; v.y = 0.0f > v.y ? 0.0f : v.y;
+                v.z = 0.0f > v.z ? 0.0f : v.z; v.w = 0.0f > v.w ? 0.0f : v.w;
+            }
+            if (epi.gate) {
+                v.x = v.x * (g[i].x > 0.0f ? 1.0f : 0.0f); v.y = v.y * (g[i].y > 0.0f ? 1.0f : 0.0f);
+                v.z = v.z * (g[i].z > 0.0f ? 1.0f : 0.0f); v.w = v.w * (g[i].w > 0.0f ? 1.0f : 0.0f);
+            }
+            st4(C + static_cast<size_t>(r) * N + j, v);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (j + c < N) store_epi(epi, C, r, j + c, N, o[c]);
+        }
+    }
 }
 
 template <bool TA, bool TB>
@@ -272,7 +511,7 @@ int launch_t(const float *A, const float *B, float *C, size_t M, size_t N, size_
              dim3 grid, unsigned tiles_n, unsigned splits, size_t kper, Epilogue epi, float *part,
              unsigned *counters, hipStream_t s) {
 #define CXM_GEMM_LAUNCH(VA_, VB_)                                                                  \
-    hipLaunchKernelGGL((k_gemm<TA, TB, VA_, VB_>), grid, dim3(kBlock), 0, s, A, B, C, M, N, K, tiles_n, \
+    hipLaunchKernelGGL((k_gemm<TA, TB, VA_, VB_>), grid, dim3(kGemmThreads), 0, s, A, B, C, M, N, K, tiles_n, \
                        splits, kper, epi, part, counters)
     if (va && vb) CXM_GEMM_LAUNCH(true, true);
     else if (va) CXM_GEMM_LAUNCH(true, false);
@@ -282,18 +521,67 @@ int launch_t(const float *A, const float *B, float *C, size_t M, size_t N, size_
     return launch_status();
 }
 
-int gemm(const float *A, const float *B, float *C, size_t M, size_t K, size_t N, int ta, int tb,
-         const float *bias, int act, const float *gate, cxm_stream_t st) {
-    if (!A || !B || !C || (act != CXM_ACT_NONE && act != CXM_ACT_RELU)) return CXM_E_INVALID;
+// Thin products; returns 1 when the shape has no thin kernel.
+int gemm_thin(const float *A, const float *B, float *C, size_t M, size_t K, size_t N, int ta, int tb,
+              const Epilogue &epi, cxm_stream_t st) {
+    hipStream_t s = reinterpret_cast<hipStream_t>(st);
+    if (N <= kThin && !tb && !ta && K % 4 == 0 && K <= 1024 && aligned16(A)) {
+        const dim3 grid(ceil_div(M, kThinNT / kWave));
+        hipLaunchKernelGGL(k_gemm_thin_n, grid, dim3(kThinNT), kThin * K * sizeof(float), s, A, B, C, M, N, K, epi);
+        return launch_status();
+    }
+    if (N <= kThin && !tb && ta && M % 4 == 0 && aligned16(A)) {
+        const size_t ntiles = (M + kColTileThin - 1) / kColTileThin;
+        size_t chunks = (256 + ntiles - 1) / ntiles;
+        const size_t max_chunks = (K + 15) / 16;
+        if (chunks > max_chunks) chunks = max_chunks;
+        if (chunks < 1) chunks = 1;
+        const size_t kpc = (K + chunks - 1) / chunks;
+        chunks = (K + kpc - 1) / kpc;
+        if (ntiles * chunks > 0x7fffffffu || N * M > 0x7fffffffu) return 1;
+        Workspace ws;
+        int rc = get_workspace(st, 0, chunks * kThin * M * sizeof(float), &ws);
+        if (rc) return rc;
+        float *part = static_cast<float *>(ws.scratch);
+        hipLaunchKernelGGL(k_gemm_thin_tn, dim3(static_cast<unsigned>(ntiles * chunks)), dim3(kBlock), 0, s, A, B, M,
+                           N, K, static_cast<unsigned>(ntiles), kpc, part);
+        if ((rc = launch_status())) return rc;
+        hipLaunchKernelGGL(k_gemm_thin_tn_sum, dim3(ceil_div(N * M, kBlock)), dim3(kBlock), 0, s, part, C, M, N,
+                           static_cast<unsigned>(chunks), epi);
+        return launch_status();
+    }
+    if (K <= kThin && !ta && N >= 64 && M < 0x7fffffffu) {
+        const size_t tiles = (N + kThinCols - 1) / kThinCols;
+        const size_t chunks = (M + kThinRows - 1) / kThinRows;
+        if (chunks > 0x7fffffffu || tiles > 65535) return 1;
+        const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(chunks));
+        if (tb) hipLaunchKernelGGL(k_gemm_thin_k<true>, grid, dim3(kThinNT), 0, s, A, B, C, M, N, K, epi);
+        else hipLaunchKernelGGL(k_gemm_thin_k<false>, grid, dim3(kThinNT), 0, s, A, B, C, M, N, K, epi);
+        return launch_status();
+    }
+    return 1;
+}
+
+}  // namespace
+
+int gemm_ex(const float *A, const float *B, float *C, size_t M, size_t K, size_t N, int ta, int tb,
+            const Epilogue &epi, cxm_stream_t st) {
+    if (!A || !B || !C || (epi.act != CXM_ACT_NONE && epi.act != CXM_ACT_RELU)) return CXM_E_INVALID;
     if (M == 0 || N == 0) return CXM_OK;
     if (K == 0) return CXM_E_INVALID;
+    {
+        const int t = gemm_thin(A, B, C, M, K, N, ta, tb, epi, st);
+        if (t != 1) return t;
+    }
     const size_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const size_t tiles = tiles_m * tiles_n;
-    // Split K when the tile grid alone cannot fill the chip; each split
-    // keeps at least 256 of K.
+    // Split K when the tile grid alone cannot fill the chip's 256 CUs;
+    // each split keeps at least 256 of K.
     size_t splits = 1;
-    if (tiles < 512 && K >= 512) {
-        splits = (512 + tiles - 1) / tiles;
+    // (at most 256 workgroups: one 8-wave workgroup fills a CU, and a 257th
+    // would run as a second round)
+    if (tiles < 192 && K >= 512) {
+        splits = 256 / tiles;
         const size_t max_splits = K / 256;
         if (splits > max_splits) splits = max_splits;
         if (splits < 1) splits = 1;
@@ -314,7 +602,6 @@ int gemm(const float *A, const float *B, float *C, size_t M, size_t K, size_t N,
     // 128-bit global loads need the stored row length to be a multiple of 4.
     const bool va = aligned16(A) && (ta ? M % 4 == 0 : K % 4 == 0);
     const bool vb = aligned16(B) && (tb ? K % 4 == 0 : N % 4 == 0);
-    const Epilogue epi{bias, gate, act};
     const dim3 grid(static_cast<unsigned>(tiles * splits));
     hipStream_t s = reinterpret_cast<hipStream_t>(st);
     const unsigned tn = static_cast<unsigned>(tiles_n), sp = static_cast<unsigned>(splits);
@@ -324,19 +611,18 @@ int gemm(const float *A, const float *B, float *C, size_t M, size_t K, size_t N,
     return launch_t<true, true>(A, B, C, M, N, K, va, vb, grid, tn, sp, kper, epi, part, counters, s);
 }
 
-}  // namespace
 }  // namespace cxm
 
 extern "C" {
 
 int cxm_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t k, size_t n, int trans_a,
                  int trans_b, const float *bias, int act, const float *gate, cxm_stream_t s) {
-    return cxm::gemm(a, b, c, m, k, n, trans_a != 0, trans_b != 0, bias, act, gate, s);
+    return cxm::gemm_ex(a, b, c, m, k, n, trans_a != 0, trans_b != 0, cxm::Epilogue{bias, gate, act, 0, 0.0f}, s);
 }
 
 int cxm_matmul_f32(const float *a, const float *b, float *c, size_t xN, size_t yN, size_t zN,
                    cxm_stream_t s) {
-    return cxm::gemm(a, b, c, xN, yN, zN, 0, 0, nullptr, CXM_ACT_NONE, nullptr, s);
+    return cxm::gemm_ex(a, b, c, xN, yN, zN, 0, 0, cxm::Epilogue{nullptr, nullptr, CXM_ACT_NONE, 0, 0.0f}, s);
 }
 
 }  // extern "C"

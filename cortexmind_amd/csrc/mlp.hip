@@ -8,12 +8,16 @@
 // (the job a chain of concrete GradientFlows would do), and SGD:
 //   h1 = relu(x W1 + b1), h2 = relu(h1 W2 + b2), logits = h2 W3 + b3
 //   loss, dlogits = softmax cross-entropy
-//   gW3 = h2^T dl, gb3 = colsum(dl), dh2 = (dl W3^T) * [h2 > 0]
-//   gW2 = h1^T dh2, gb2 = colsum(dh2), dh1 = (dh2 W2^T) * [h1 > 0]
+//   dh2 = (dl W3^T) * [h2 > 0], gW3 = h2^T dl, gb3 = colsum(dl)
+//   dh1 = (dh2 W2^T) * [h1 > 0], gW2 = h1^T dh2, gb2 = colsum(dh2)
 //   gW1 = x^T dh1, gb1 = colsum(dh1)
-//   W -= lr * gW, b -= lr * gb (all six after every gradient exists)
-// Bias add and ReLU ride in the forward GEMM epilogue; the ReLU backward
-// mask rides in the dX GEMM epilogue.  Everything is enqueued on one
+//   W -= lr * gW, b -= lr * gb
+// Bias add and ReLU ride in the forward GEMM epilogue, the ReLU backward
+// mask in the dX GEMM epilogue, and each SGD update in the epilogue of the
+// kernel that produces its gradient (weights: the dW GEMM; biases: the
+// column sum), so no gradient is ever written out.  A layer's weights are
+// updated only after its dX product has read them, which gives the same
+// values as taking every gradient first.  Everything is enqueued on one
 // stream without host synchronisation.
 #include <new>
 
@@ -22,7 +26,6 @@
 struct cxm_mlp3 {
     size_t b, d0, d1, d2, d3;
     float *h1, *h2, *lg, *dl, *dh2, *dh1;
-    float *gw1, *gw2, *gw3, *gb1, *gb2, *gb3;
     void *block;  // one allocation holding all of the above
 };
 
@@ -40,9 +43,8 @@ int cxm_mlp3_create(cxm_mlp3 **handle, size_t batch, size_t d0, size_t d1, size_
     h->d3 = d3;
     // sizes in floats, each rounded to 64 floats (256 B) to keep 128-bit alignment
     auto r = [](size_t n) { return (n + 63) / 64 * 64; };
-    const size_t sizes[12] = {r(batch * d1), r(batch * d2), r(batch * d3), r(batch * d3),
-                              r(batch * d2), r(batch * d1), r(d0 * d1),    r(d1 * d2),
-                              r(d2 * d3),    r(d1),         r(d2),         r(d3)};
+    const size_t sizes[6] = {r(batch * d1), r(batch * d2), r(batch * d3),
+                             r(batch * d3), r(batch * d2), r(batch * d1)};
     size_t total = 0;
     for (size_t s : sizes) total += s;
     void *p = nullptr;
@@ -53,9 +55,8 @@ int cxm_mlp3_create(cxm_mlp3 **handle, size_t batch, size_t d0, size_t d1, size_
     }
     h->block = p;
     float *f = static_cast<float *>(p);
-    float **slots[12] = {&h->h1, &h->h2, &h->lg, &h->dl, &h->dh2, &h->dh1,
-                         &h->gw1, &h->gw2, &h->gw3, &h->gb1, &h->gb2, &h->gb3};
-    for (int i = 0; i < 12; ++i) {
+    float **slots[6] = {&h->h1, &h->h2, &h->lg, &h->dl, &h->dh2, &h->dh1};
+    for (int i = 0; i < 6; ++i) {
         *slots[i] = f;
         f += sizes[i];
     }
@@ -79,29 +80,24 @@ int cxm_mlp3_step_f32(cxm_mlp3 *h, const float *x, const int32_t *labels, float 
 #define CXM_TRY(call)        \
     if ((rc = (call)) != 0) \
         return rc
+    using cxm::Epilogue;
+    const Epilogue sgd{nullptr, nullptr, CXM_ACT_NONE, 1, lr};
     // forward
-    CXM_TRY(cxm_gemm_f32(x, w1, h->h1, B, d0, d1, 0, 0, b1, CXM_ACT_RELU, nullptr, s));
-    CXM_TRY(cxm_gemm_f32(h->h1, w2, h->h2, B, d1, d2, 0, 0, b2, CXM_ACT_RELU, nullptr, s));
-    CXM_TRY(cxm_gemm_f32(h->h2, w3, h->lg, B, d2, d3, 0, 0, b3, CXM_ACT_NONE, nullptr, s));
+    CXM_TRY(cxm::gemm_ex(x, w1, h->h1, B, d0, d1, 0, 0, Epilogue{b1, nullptr, CXM_ACT_RELU, 0, 0.0f}, s));
+    CXM_TRY(cxm::gemm_ex(h->h1, w2, h->h2, B, d1, d2, 0, 0, Epilogue{b2, nullptr, CXM_ACT_RELU, 0, 0.0f}, s));
+    CXM_TRY(cxm::gemm_ex(h->h2, w3, h->lg, B, d2, d3, 0, 0, Epilogue{b3, nullptr, CXM_ACT_NONE, 0, 0.0f}, s));
     CXM_TRY(cxm_softmax_xent_f32(h->lg, labels, loss, h->dl, B, d3, s));
-    // backward, layer 3
-    CXM_TRY(cxm_gemm_f32(h->h2, h->dl, h->gw3, d2, B, d3, 1, 0, nullptr, CXM_ACT_NONE, nullptr, s));
-    CXM_TRY(cxm_reduce_sum_f32(h->dl, h->gb3, 1, B, d3, s));
-    CXM_TRY(cxm_gemm_f32(h->dl, w3, h->dh2, B, d3, d2, 0, 1, nullptr, CXM_ACT_NONE, h->h2, s));
+    // layer 3: dX first (reads W3), then W3 -= lr * h2^T dl, b3 -= lr * colsum(dl)
+    CXM_TRY(cxm::gemm_ex(h->dl, w3, h->dh2, B, d3, d2, 0, 1, Epilogue{nullptr, h->h2, CXM_ACT_NONE, 0, 0.0f}, s));
+    CXM_TRY(cxm::gemm_ex(h->h2, h->dl, w3, d2, B, d3, 1, 0, sgd, s));
+    CXM_TRY(cxm::colsum_sgd(h->dl, b3, B, d3, lr, s));
     // layer 2
-    CXM_TRY(cxm_gemm_f32(h->h1, h->dh2, h->gw2, d1, B, d2, 1, 0, nullptr, CXM_ACT_NONE, nullptr, s));
-    CXM_TRY(cxm_reduce_sum_f32(h->dh2, h->gb2, 1, B, d2, s));
-    CXM_TRY(cxm_gemm_f32(h->dh2, w2, h->dh1, B, d2, d1, 0, 1, nullptr, CXM_ACT_NONE, h->h1, s));
+    CXM_TRY(cxm::gemm_ex(h->dh2, w2, h->dh1, B, d2, d1, 0, 1, Epilogue{nullptr, h->h1, CXM_ACT_NONE, 0, 0.0f}, s));
+    CXM_TRY(cxm::gemm_ex(h->h1, h->dh2, w2, d1, B, d2, 1, 0, sgd, s));
+    CXM_TRY(cxm::colsum_sgd(h->dh2, b2, B, d2, lr, s));
     // layer 1
-    CXM_TRY(cxm_gemm_f32(x, h->dh1, h->gw1, d0, B, d1, 1, 0, nullptr, CXM_ACT_NONE, nullptr, s));
-    CXM_TRY(cxm_reduce_sum_f32(h->dh1, h->gb1, 1, B, d1, s));
-    // SGD
-    CXM_TRY(cxm_sgd_f32(w1, h->gw1, lr, d0 * d1, s));
-    CXM_TRY(cxm_sgd_f32(b1, h->gb1, lr, d1, s));
-    CXM_TRY(cxm_sgd_f32(w2, h->gw2, lr, d1 * d2, s));
-    CXM_TRY(cxm_sgd_f32(b2, h->gb2, lr, d2, s));
-    CXM_TRY(cxm_sgd_f32(w3, h->gw3, lr, d2 * d3, s));
-    CXM_TRY(cxm_sgd_f32(b3, h->gb3, lr, d3, s));
+    CXM_TRY(cxm::gemm_ex(x, h->dh1, w1, d0, B, d1, 1, 0, sgd, s));
+    CXM_TRY(cxm::colsum_sgd(h->dh1, b1, B, d1, lr, s));
 #undef CXM_TRY
     return CXM_OK;
 }

@@ -29,13 +29,13 @@ struct MaxColOp : MaxOp {
     __device__ static T identity() { return -INFINITY; }
 };
 
-enum OutKind : int { kOutValue = 0, kOutMean = 1, kOutIndex = 2 };
+enum OutKind : int { kOutValue = 0, kOutMean = 1, kOutIndex = 2, kOutSgd = 3 };
 
 struct OutDesc {
     void *z;
     int kind;
     size_t body;  // mean: outputs [0, body) multiply by inv, the rest divide by dimf
-    float inv;
+    float inv;    // sgd: the learning rate
     float dimf;
 };
 
@@ -45,8 +45,14 @@ __device__ __forceinline__ void write_out(const OutDesc &o, size_t q, typename O
         static_cast<int32_t *>(o.z)[q] = r.i;
     } else {
         float v = r;
+        float *z = static_cast<float *>(o.z);
+        if (o.kind == kOutSgd) {  // z is a bias: z - sum*lr, two roundings
+            const float t = v * o.inv;
+            z[q] = z[q] - t;
+            return;
+        }
         if (o.kind == kOutMean) v = q < o.body ? v * o.inv : v / o.dimf;
-        static_cast<float *>(o.z)[q] = v;
+        z[q] = v;
     }
 }
 
@@ -382,6 +388,14 @@ int reduce_flat(Which which, const float *x, void *z, size_t n, cxm_stream_t s) 
 }
 
 }  // namespace
+
+int colsum_sgd(const float *x, float *b, size_t rows, size_t cols, float lr, cxm_stream_t s) {
+    if (!x || !b || rows == 0) return CXM_E_INVALID;
+    if (cols == 0) return CXM_OK;
+    OutDesc out{b, kOutSgd, 0, lr, 0.0f};
+    return run_cols<SumOp>(x, 1, rows, cols, out, s);
+}
+
 }  // namespace cxm
 
 extern "C" {

@@ -91,3 +91,25 @@ def test_bad_arguments(hip):
     assert lib().cxm_gemm_f32(None, None, None, 4, 4, 4, 0, 0, None, 0, None, None) == E_INVALID
     d = empty((16,))
     assert lib().cxm_gemm_f32(d.ptr, d.ptr, d.ptr, 4, 4, 4, 0, 0, None, 7, None, None) == E_INVALID
+
+
+@pytest.mark.parametrize("m,k,n,ta,tb", [(4096, 1024, 10, 0, 0), (1024, 4096, 10, 1, 0), (4096, 10, 1024, 0, 1),
+                                         (4096, 10, 1024, 0, 0), (77, 100, 3, 0, 0), (64, 333, 16, 1, 0),
+                                         (50, 16, 36, 0, 1)])
+def test_thin_products(hip, orc, m, k, n, ta, tb):
+    """Shapes with a dimension <= 16 (the MLP's 10-class layer) run thin
+    kernels instead of MFMA tiles; same bar, with their epilogues."""
+    g = SplitMix64(m + 3 * k + 7 * n + ta + 2 * tb)
+    a, b = g.normal((m, k)), g.normal((k, n))
+    got = run(a, b, ta, tb)
+    ref = orc.gemm(stored(a, ta), stored(b, tb), bool(ta), bool(tb))
+    assert np.all(np.abs(got - ref) <= bound(a, b))
+    if not ta:
+        bias = g.normal((n,), 0.0, 0.5)
+        gate = g.normal((m, n))
+        z = orc.bcast_row(ref, bias, 0)
+        got_b = run(a, b, ta, tb, bias=bias, act=ACT_RELU)
+        assert np.all(np.abs(got_b - np.where(0 > z, 0, z)) <= bound(a, b))
+        got_g = run(a, b, ta, tb, gate=gate)
+        assert np.all(np.abs(got_g - ref * (gate > 0)) <= bound(a, b))
+        assert np.all(got_g[gate <= 0] == 0)
