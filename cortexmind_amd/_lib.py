@@ -21,7 +21,9 @@ E_INVALID = -1
 E_TOO_LARGE = -2
 E_NO_DEVICE = -3
 
-OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_MAX, OP_MIN = range(6)
+OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_MAX, OP_MIN, OP_POW = range(7)
+(FN_SQUARE, FN_SQRT, FN_RSQRT, FN_LOG, FN_EXP, FN_ERF, FN_SIN, FN_COS, FN_ABS, FN_NEG, FN_RCP,
+ FN_INVERSE, FN_SIGN) = range(13)
 ACT_NONE, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_EXP = range(5)
 
 _P = ctypes.c_void_p  # device pointer, stream or event handle
@@ -63,6 +65,11 @@ SIGNATURES = {
     "cxm_bcast_col_f32": [_P, _P, _P, _SZ, _SZ, _I, _P],
     "cxm_scalar_f32": [_P, _F, _P, _SZ, _I, _P],
     "cxm_unary_f32": [_P, _P, _SZ, _I, _P],
+    "cxm_wise_f32": [_P, _P, _SZ, _I, _P],
+    "cxm_lerp_f32": [_P, _F, _F, _P, _SZ, _P],
+    "cxm_clamp_f32": [_P, _F, _F, _P, _SZ, _P],
+    "cxm_gather_f32": [_P, _SZ, _P, _P, _SZ, _P],
+    "cxm_gather_i32": [_P, _SZ, _P, _P, _SZ, _P],
     "cxm_affine_act_fwd_f32": [_P, _P, _P, _P, _SZ, _SZ, _I, _P],
     "cxm_affine_act_bwd_f32": [_P, _P, _P, _P, _P, _P, _P, _SZ, _SZ, _I, _P],
     "cxm_softmax_fwd_f32": [_P, _P, _SZ, _SZ, _I, _P],

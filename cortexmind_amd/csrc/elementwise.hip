@@ -1,4 +1,4 @@
-// Elementwise fp32 kernels: same-shape binary ops, row/column broadcast,
+// Elementwise fp32 kernels: same-shape binary ops (pow included), row/column broadcast,
 // tensor-op-scalar, unary activations, the fused affine + activation
 // forward/backward of the C3 workload, and the SGD update.
 //
@@ -24,7 +24,8 @@ __device__ __forceinline__ float bin(int op, float a, float b) {
         case CXM_OP_MUL: return a * b;
         case CXM_OP_DIV: return a / b;
         case CXM_OP_MAX: return a > b ? a : b;
-        default: return a < b ? a : b;
+        case CXM_OP_MIN: return a < b ? a : b;
+        default: return powf(a, b);
     }
 }
 
@@ -35,7 +36,8 @@ __device__ __forceinline__ float bin_t(float a, float b) {
     else if constexpr (OP == CXM_OP_MUL) return a * b;
     else if constexpr (OP == CXM_OP_DIV) return a / b;
     else if constexpr (OP == CXM_OP_MAX) return a > b ? a : b;
-    else return a < b ? a : b;
+    else if constexpr (OP == CXM_OP_MIN) return a < b ? a : b;
+    else return powf(a, b);
 }
 
 template <int OP>
@@ -251,32 +253,40 @@ __global__ __launch_bounds__(kBlock) void k_affine_fwd_scalar(const float *x, co
 // ----------------------------------------------------- affine backward
 
 // dz = dy*act'(y); dx = dz*scale[j]; dscale[j] = sum_i dz*x; dbias[j] = sum_i dz.
-// Workgroup = 256 columns (64 lanes x float4) x a chunk of rows; the four
+// Workgroup = 256 columns (64 lanes x float4) x a chunk of rows; its NW
 // waves take interleaved rows and meet in LDS; chunks are combined in
-// chunk order by the last workgroup of the column tile.
+// chunk order by the last workgroup of the column tile.  With tile_major
+// the chunks of a tile are adjacent in launch order, so early tiles'
+// combines overlap later tiles' streaming.
 constexpr int kAffTile = 256;
 
-template <int ACT, bool VEC, int UNR>
-__global__ __launch_bounds__(kBlock) void k_affine_bwd(const float *__restrict__ x,
-                                                       const float *__restrict__ scale,
-                                                       const float *__restrict__ y,
-                                                       const float *__restrict__ dy,
-                                                       float *__restrict__ dx,
-                                                       float *__restrict__ dscale,
-                                                       float *__restrict__ dbias, size_t m, size_t n,
-                                                       unsigned ntiles, unsigned chunks,
-                                                       size_t rows_per_chunk,
-                                                       float *__restrict__ part,
-                                                       unsigned *__restrict__ counters) {
-    __shared__ float lds_s[kWavesPerBlock][kAffTile];
-    __shared__ float lds_b[kWavesPerBlock][kAffTile];
+template <int ACT, bool VEC, int UNR, int NW>
+__global__ __launch_bounds__(NW * kWave) void k_affine_bwd(const float *__restrict__ x,
+                                                           const float *__restrict__ scale,
+                                                           const float *__restrict__ y,
+                                                           const float *__restrict__ dy,
+                                                           float *__restrict__ dx,
+                                                           float *__restrict__ dscale,
+                                                           float *__restrict__ dbias, size_t m, size_t n,
+                                                           unsigned ntiles, unsigned chunks,
+                                                           size_t rows_per_chunk, int tile_major,
+                                                           float *__restrict__ part,
+                                                           unsigned *__restrict__ counters) {
+    constexpr int NSLOT = VEC ? NW : NW / 4;
+    __shared__ float lds_s[NSLOT][kAffTile];
+    __shared__ float lds_b[NSLOT][kAffTile];
     __shared__ int flag;
-    const unsigned tile = blockIdx.x % ntiles;
-    const unsigned chunk = blockIdx.x / ntiles;
+    unsigned tile, chunk;
+    if (tile_major) {
+        chunk = blockIdx.x % chunks;
+        tile = blockIdx.x / chunks;
+    } else {
+        tile = blockIdx.x % ntiles;
+        chunk = blockIdx.x / ntiles;
+    }
     const int tid = threadIdx.x;
     const size_t r0 = static_cast<size_t>(chunk) * rows_per_chunk;
     const size_t r1 = r0 + rows_per_chunk < m ? r0 + rows_per_chunk : m;
-    float ms, mb;  // this thread's column (tile*256 + tid) over the chunk
 
     if constexpr (VEC) {
         const int lane = tid & (kWave - 1);
@@ -297,19 +307,19 @@ __global__ __launch_bounds__(kBlock) void k_affine_bwd(const float *__restrict__
                 as[0] = as[0] + p0; as[1] = as[1] + p1; as[2] = as[2] + p2; as[3] = as[3] + p3;
                 ab[0] = ab[0] + dz.x; ab[1] = ab[1] + dz.y; ab[2] = ab[2] + dz.z; ab[3] = ab[3] + dz.w;
             };
-            for (; r + (UNR - 1) * kWavesPerBlock < r1; r += UNR * kWavesPerBlock) {
+            for (; r + (UNR - 1) * NW < r1; r += UNR * NW) {
                 float4 xv[UNR], yv[UNR], gv[UNR];
 #pragma unroll
                 for (int u = 0; u < UNR; ++u) {
-                    const size_t o = (r + u * kWavesPerBlock) * n + col;
+                    const size_t o = (r + u * NW) * n + col;
                     xv[u] = ld4_stream(x + o);
                     yv[u] = ld4_stream(y + o);
                     gv[u] = ld4_stream(dy + o);
                 }
 #pragma unroll
-                for (int u = 0; u < UNR; ++u) body(r + u * kWavesPerBlock, xv[u], yv[u], gv[u]);
+                for (int u = 0; u < UNR; ++u) body(r + u * NW, xv[u], yv[u], gv[u]);
             }
-            for (; r < r1; r += kWavesPerBlock) {
+            for (; r < r1; r += NW) {
                 const size_t o = r * n + col;
                 body(r, ld4_stream(x + o), ld4_stream(y + o), ld4_stream(dy + o));
             }
@@ -319,16 +329,13 @@ __global__ __launch_bounds__(kBlock) void k_affine_bwd(const float *__restrict__
             lds_s[w][lane * 4 + c] = as[c];
             lds_b[w][lane * 4 + c] = ab[c];
         }
-        __syncthreads();
-        ms = (lds_s[0][tid] + lds_s[1][tid]) + (lds_s[2][tid] + lds_s[3][tid]);
-        mb = (lds_b[0][tid] + lds_b[1][tid]) + (lds_b[2][tid] + lds_b[3][tid]);
     } else {
-        const size_t col = static_cast<size_t>(tile) * kAffTile + tid;
-        ms = 0.0f;
-        mb = 0.0f;
+        const int c = tid % kAffTile, ph = tid / kAffTile;
+        const size_t col = static_cast<size_t>(tile) * kAffTile + c;
+        float ms = 0.0f, mb = 0.0f;
         if (col < n) {
             const float sc = scale[col];
-            for (size_t r = r0; r < r1; ++r) {
+            for (size_t r = r0 + ph; r < r1; r += NSLOT) {
                 const size_t o = r * n + col;
                 const float dz = dy[o] * dact<ACT>(y[o]);
                 dx[o] = dz * sc;
@@ -337,25 +344,54 @@ __global__ __launch_bounds__(kBlock) void k_affine_bwd(const float *__restrict__
                 mb = mb + dz;
             }
         }
+        lds_s[ph][c] = ms;
+        lds_b[ph][c] = mb;
     }
-
+    __syncthreads();
+    const bool owner = tid < kAffTile;  // threads 0..255 own one column each from here
+    float ms = 0.0f, mb = 0.0f;
+    if (owner) {
+#pragma unroll
+        for (int k = 0; k < NSLOT; ++k) {  // slots in order
+            ms = ms + lds_s[k][tid];
+            mb = mb + lds_b[k][tid];
+        }
+    }
     const size_t col = static_cast<size_t>(tile) * kAffTile + tid;
     if (chunks == 1) {
-        if (col < n) {
+        if (owner && col < n) {
             dscale[col] = ms;
             dbias[col] = mb;
         }
         return;
     }
     const size_t slot = static_cast<size_t>(tile) * chunks;
-    st_dev(&part[((slot + chunk) * 2 + 0) * kAffTile + tid], ms);
-    st_dev(&part[((slot + chunk) * 2 + 1) * kAffTile + tid], mb);
+    if (owner) {
+        st_dev(&part[((slot + chunk) * 2 + 0) * kAffTile + tid], ms);
+        st_dev(&part[((slot + chunk) * 2 + 1) * kAffTile + tid], mb);
+    }
     if (!last_block_ticket(ctr(counters, tile), chunks, &flag)) return;
-    const float a = combine_partials<SumOp>(part + (slot * 2 + 0) * kAffTile + tid, chunks, 2 * kAffTile, 0.0f);
-    const float bsum = combine_partials<SumOp>(part + (slot * 2 + 1) * kAffTile + tid, chunks, 2 * kAffTile, 0.0f);
-    if (col < n) {
-        dscale[col] = a;
-        dbias[col] = bsum;
+    if (owner) {
+        // both sums' loads go out together, 8 chunks at a time
+        float a = 0.0f, bsum = 0.0f;
+        for (unsigned c0 = 0; c0 < chunks; c0 += 8) {
+            float va[8], vb[8];
+#pragma unroll
+            for (unsigned u = 0; u < 8; ++u) {
+                const bool in = c0 + u < chunks;
+                va[u] = in ? ld_dev(&part[((slot + c0 + u) * 2 + 0) * kAffTile + tid]) : 0.0f;
+                vb[u] = in ? ld_dev(&part[((slot + c0 + u) * 2 + 1) * kAffTile + tid]) : 0.0f;
+            }
+#pragma unroll
+            for (unsigned u = 0; u < 8; ++u) {
+                a = a + va[u];
+                bsum = bsum + vb[u];
+            }
+        }
+        if (col < n) {
+            dscale[col] = a;
+            dbias[col] = bsum;
+        }
     }
 }
 
@@ -402,6 +438,7 @@ int dispatch_op(int op, A... a) {
         case CXM_OP_DIV: return L<CXM_OP_DIV>::run(a...);
         case CXM_OP_MAX: return L<CXM_OP_MAX>::run(a...);
         case CXM_OP_MIN: return L<CXM_OP_MIN>::run(a...);
+        case CXM_OP_POW: return L<CXM_OP_POW>::run(a...);
         default: return CXM_E_INVALID;
     }
 }
@@ -486,18 +523,29 @@ int affine_fwd_t(const float *x, const float *scale, const float *bias, float *y
     return launch_status();
 }
 
+// Row chunks per column tile and launch order.  Measured on gfx950 at 256 MiB
+// per operand: 512 workgroups of 4 waves (two per CU, each streaming a few
+// hundred rows) reach 6.1-6.2 TB/s at [8192, 8192] and [1024, 65536], where
+// 2048 shorter workgroups stay near 5.4 TB/s and 384 leave CUs unevenly
+// loaded; 16-wave workgroups were slower at every square or wide shape.
+struct AffBwdPlan {
+    size_t chunks;   // 0: enough for about 512 workgroups
+    int tile_major;  // chunks of one tile adjacent in launch order
+};
+
 template <int ACT>
-int affine_bwd_t(const float *x, const float *scale, const float *y, const float *dy, float *dx,
-                 float *dscale, float *dbias, size_t m, size_t n, cxm_stream_t st) {
+int affine_bwd_plan(const float *x, const float *scale, const float *y, const float *dy, float *dx,
+                    float *dscale, float *dbias, size_t m, size_t n, AffBwdPlan plan, cxm_stream_t st) {
     const bool vec = n % 4 == 0 && aligned16(x) && aligned16(scale) && aligned16(y) &&
                      aligned16(dy) && aligned16(dx);
     const size_t ntiles = (n + kAffTile - 1) / kAffTile;
-    size_t chunks = (2048 + ntiles - 1) / ntiles;
+    size_t chunks = plan.chunks;
+    if (chunks == 0) chunks = (512 + ntiles - 1) / ntiles;
     const size_t max_chunks = (m + 15) / 16;
     if (chunks > max_chunks) chunks = max_chunks;
     if (chunks < 1) chunks = 1;
     size_t rpc = (m + chunks - 1) / chunks;
-    rpc = (rpc + 3) / 4 * 4;
+    rpc = (rpc + 15) / 16 * 16;
     chunks = (m + rpc - 1) / rpc;
     if (chunks < 1) chunks = 1;
     if (ntiles * chunks > 0x7fffffffu) return CXM_E_TOO_LARGE;
@@ -511,15 +559,20 @@ int affine_bwd_t(const float *x, const float *scale, const float *y, const float
         counters = ws.counters;
     }
     const dim3 grid(static_cast<unsigned>(ntiles * chunks));
-    if (vec)
-        hipLaunchKernelGGL((k_affine_bwd<ACT, true, 4>), grid, dim3(kBlock), 0, hs(st), x, scale, y,
-                           dy, dx, dscale, dbias, m, n, static_cast<unsigned>(ntiles),
-                           static_cast<unsigned>(chunks), rpc, part, counters);
-    else
-        hipLaunchKernelGGL((k_affine_bwd<ACT, false, 1>), grid, dim3(kBlock), 0, hs(st), x, scale, y,
-                           dy, dx, dscale, dbias, m, n, static_cast<unsigned>(ntiles),
-                           static_cast<unsigned>(chunks), rpc, part, counters);
+    const unsigned nt = static_cast<unsigned>(ntiles), nc = static_cast<unsigned>(chunks);
+#define CXM_AFFB(VEC_, UNR_, NW_)                                                                       \
+    hipLaunchKernelGGL((k_affine_bwd<ACT, VEC_, UNR_, NW_>), grid, dim3(NW_ * kWave), 0, hs(st), x, scale, y, dy, \
+                       dx, dscale, dbias, m, n, nt, nc, rpc, plan.tile_major, part, counters)
+    if (vec) CXM_AFFB(true, 4, 4);
+    else CXM_AFFB(false, 1, 4);
+#undef CXM_AFFB
     return launch_status();
+}
+
+template <int ACT>
+int affine_bwd_t(const float *x, const float *scale, const float *y, const float *dy, float *dx,
+                 float *dscale, float *dbias, size_t m, size_t n, cxm_stream_t st) {
+    return affine_bwd_plan<ACT>(x, scale, y, dy, dx, dscale, dbias, m, n, AffBwdPlan{0, 1}, st);
 }
 
 }  // namespace
@@ -530,7 +583,7 @@ using namespace cxm;
 extern "C" {
 
 int cxm_binary_f32(const float *x, const float *y, float *z, size_t n, int op, cxm_stream_t s) {
-    if (!x || !y || !z || op < CXM_OP_ADD || op > CXM_OP_MIN) return CXM_E_INVALID;
+    if (!x || !y || !z || op < CXM_OP_ADD || op > CXM_OP_POW) return CXM_E_INVALID;
     if (n == 0) return CXM_OK;
     if (aligned16(x) && aligned16(y) && aligned16(z)) return dispatch_op<BinaryL>(op, x, y, z, n, hs(s));
     hipLaunchKernelGGL(k_binary_scalar, dim3(stream_grid((n + 3) / 4)), dim3(kBlock), 0, hs(s), x, y, z,
@@ -549,7 +602,7 @@ int cxm_bcast_col_f32(const float *x, const float *y, float *z, size_t m, size_t
 }
 
 int cxm_scalar_f32(const float *x, float value, float *z, size_t n, int op, cxm_stream_t s) {
-    if (!x || !z || op < CXM_OP_ADD || op > CXM_OP_MIN) return CXM_E_INVALID;
+    if (!x || !z || op < CXM_OP_ADD || op > CXM_OP_POW) return CXM_E_INVALID;
     if (n == 0) return CXM_OK;
     if (aligned16(x) && aligned16(z)) return dispatch_op<ScalarL>(op, x, value, z, n, hs(s));
     hipLaunchKernelGGL(k_scalar_scalar, dim3(stream_grid((n + 3) / 4)), dim3(kBlock), 0, hs(s), x, value,

@@ -1,0 +1,181 @@
+// Elementwise math surface: z = fn(x) for the unary functions of the
+// reference's GPU and CPU engines, plus lerp, clamp and gather.
+//
+// Replaces kernels::Unary<Op> (source/CortexMind/framework/Engine/Kernels/
+// unary.cuh:16-40) as instantiated by nv::ElementWise (Engine/CUDA/
+// element_wise.cu:17-181), and the fp32 branch of avx2::wise (Engine/AVX2/
+// wise.cpp:56-194).  pow lives with the binary/scalar operator kernels.
+//
+// Each function is the correctly rounded IEEE operation where one exists
+// (x*x, sqrt, 1/x, |x|, -x); rsqrt is 1/sqrt(x), two correctly rounded
+// steps; log/exp/erf/sin/cos are the device math library's functions.  The
+// reference's AVX2 body uses 12-bit approximations for rcp and rsqrt
+// (_mm256_rcp_ps / _mm256_rsqrt_ps, functions.hpp:168-170, 240-242) and its
+// CUDA build compiles with --use_fast_math; the results here are at least as
+// accurate as either.
+#include "cxm_common.hpp"
+
+namespace cxm {
+namespace {
+
+struct FSquare { __device__ float operator()(float x) const { return x * x; } };
+struct FSqrt { __device__ float operator()(float x) const { return __builtin_sqrtf(x); } };
+struct FRsqrt {
+    __device__ float operator()(float x) const {
+        const float r = __builtin_sqrtf(x);
+        return 1.0f / r;
+    }
+};
+struct FLog { __device__ float operator()(float x) const { return logf(x); } };
+struct FExp { __device__ float operator()(float x) const { return expf(x); } };
+struct FErf { __device__ float operator()(float x) const { return erff(x); } };
+struct FSin { __device__ float operator()(float x) const { return sinf(x); } };
+struct FCos { __device__ float operator()(float x) const { return cosf(x); } };
+struct FAbs { __device__ float operator()(float x) const { return fabsf(x); } };
+struct FNeg { __device__ float operator()(float x) const { return -x; } };
+struct FRcp { __device__ float operator()(float x) const { return 1.0f / x; } };
+// (x > 0) - (x < 0): Operations/kernel_ops.cuh:268-274
+struct FSign {
+    __device__ float operator()(float x) const {
+        return static_cast<float>(static_cast<int>(x > 0.0f) - static_cast<int>(x < 0.0f));
+    }
+};
+// fma(t, b - a, a) with a = x, b = v1, t = v2: functions.hpp:271-274
+struct FLerp {
+    float v1, v2;
+    __device__ float operator()(float x) const {
+        const float d = v1 - x;
+        return fmaf(v2, d, x);
+    }
+};
+// min(max(x, lo), hi) with the SIMD operand rule max(a, b) = a > b ? a : b,
+// min(a, b) = a < b ? a : b: functions.hpp:332-335
+struct FClamp {
+    float lo, hi;
+    __device__ float operator()(float x) const {
+        const float m = x > lo ? x : lo;
+        return m < hi ? m : hi;
+    }
+};
+
+template <class F>
+__device__ __forceinline__ float4 map4(const F &f, float4 v) {
+    return make_float4(f(v.x), f(v.y), f(v.z), f(v.w));
+}
+
+// 16-byte aligned x and z: float4 grid-stride body, two float4 per thread
+// per iteration, tail (n % 4) by the first threads of workgroup 0.  z may
+// alias x: every element is read and written by the same thread.
+template <class F>
+__global__ __launch_bounds__(kBlock) void k_map_vec(F f, const float *x, float *z, size_t n) {
+    const size_t n4 = n / 4;
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    for (; i + stride < n4; i += 2 * stride) {
+        const float4 a = ld4(x + 4 * i), b = ld4(x + 4 * (i + stride));
+        st4(z + 4 * i, map4(f, a));
+        st4(z + 4 * (i + stride), map4(f, b));
+    }
+    if (i < n4) st4(z + 4 * i, map4(f, ld4(x + 4 * i)));
+    if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
+        const size_t j = 4 * n4 + threadIdx.x;
+        z[j] = f(x[j]);
+    }
+}
+
+template <class F>
+__global__ __launch_bounds__(kBlock) void k_map_any(F f, const float *x, float *z, size_t n) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+        z[i] = f(x[i]);
+}
+
+// Same launch shape as the other streaming kernels: at most 16 workgroups
+// per CU, each thread striding through the rest.
+inline unsigned map_grid(size_t units) {
+    size_t b = (units + kBlock - 1) / kBlock;
+    const size_t cap = 256 * 16;
+    return static_cast<unsigned>(b < 1 ? 1 : (b > cap ? cap : b));
+}
+
+inline hipStream_t hs(cxm_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+template <class F>
+int map(F f, const float *x, float *z, size_t n, cxm_stream_t s) {
+    if (aligned16(x) && aligned16(z))
+        hipLaunchKernelGGL(k_map_vec<F>, dim3(map_grid((n / 4 + 1) / 2)), dim3(kBlock), 0, hs(s), f, x, z, n);
+    else
+        hipLaunchKernelGGL(k_map_any<F>, dim3(map_grid(n)), dim3(kBlock), 0, hs(s), f, x, z, n);
+    return launch_status();
+}
+
+// z[i] = x[idx[i]]; an index outside [0, xn) gives `bad` and reads nothing.
+template <class T>
+__global__ __launch_bounds__(kBlock) void k_gather(const T *__restrict__ x, size_t xn,
+                                                   const int32_t *__restrict__ idx, T *z, size_t n,
+                                                   T bad) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        const int32_t k = idx[i];
+        z[i] = (k >= 0 && static_cast<size_t>(k) < xn) ? x[k] : bad;
+    }
+}
+
+}  // namespace
+}  // namespace cxm
+
+using namespace cxm;
+
+extern "C" {
+
+int cxm_wise_f32(const float *x, float *z, size_t n, int fn, cxm_stream_t s) {
+    if (!x || !z || fn < CXM_FN_SQUARE || fn > CXM_FN_SIGN) return CXM_E_INVALID;
+    if (n == 0) return CXM_OK;
+    switch (fn) {
+        case CXM_FN_SQUARE: return map(FSquare{}, x, z, n, s);
+        case CXM_FN_SQRT: return map(FSqrt{}, x, z, n, s);
+        case CXM_FN_RSQRT: return map(FRsqrt{}, x, z, n, s);
+        case CXM_FN_LOG: return map(FLog{}, x, z, n, s);
+        case CXM_FN_EXP: return map(FExp{}, x, z, n, s);
+        case CXM_FN_ERF: return map(FErf{}, x, z, n, s);
+        case CXM_FN_SIN: return map(FSin{}, x, z, n, s);
+        case CXM_FN_COS: return map(FCos{}, x, z, n, s);
+        case CXM_FN_ABS: return map(FAbs{}, x, z, n, s);
+        case CXM_FN_NEG: return map(FNeg{}, x, z, n, s);
+        case CXM_FN_RCP:
+        case CXM_FN_INVERSE: return map(FRcp{}, x, z, n, s);
+        default: return map(FSign{}, x, z, n, s);
+    }
+}
+
+int cxm_lerp_f32(const float *x, float v1, float v2, float *z, size_t n, cxm_stream_t s) {
+    if (!x || !z) return CXM_E_INVALID;
+    if (n == 0) return CXM_OK;
+    return map(FLerp{v1, v2}, x, z, n, s);
+}
+
+int cxm_clamp_f32(const float *x, float lo, float hi, float *z, size_t n, cxm_stream_t s) {
+    if (!x || !z) return CXM_E_INVALID;
+    if (n == 0) return CXM_OK;
+    return map(FClamp{lo, hi}, x, z, n, s);
+}
+
+int cxm_gather_f32(const float *x, size_t x_n, const int32_t *idx, float *z, size_t n,
+                   cxm_stream_t s) {
+    if (!x || !idx || !z) return CXM_E_INVALID;
+    if (n == 0) return CXM_OK;
+    hipLaunchKernelGGL(k_gather<float>, dim3(map_grid(n)), dim3(kBlock), 0, hs(s), x, x_n, idx, z, n,
+                       __builtin_nanf(""));
+    return launch_status();
+}
+
+int cxm_gather_i32(const int32_t *x, size_t x_n, const int32_t *idx, int32_t *z, size_t n,
+                   cxm_stream_t s) {
+    if (!x || !idx || !z) return CXM_E_INVALID;
+    if (n == 0) return CXM_OK;
+    hipLaunchKernelGGL(k_gather<int32_t>, dim3(map_grid(n)), dim3(kBlock), 0, hs(s), x, x_n, idx, z, n,
+                       INT32_MIN);
+    return launch_status();
+}
+
+}  // extern "C"

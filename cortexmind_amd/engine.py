@@ -12,10 +12,13 @@ from __future__ import annotations
 
 import ctypes
 
-from ._lib import (ACT_EXP, ACT_NONE, ACT_RELU, ACT_SIGMOID, ACT_TANH, OP_ADD, OP_DIV, OP_MAX,
-                   OP_MIN, OP_MUL, OP_SUB, call)
+import numpy as np
 
-__all__ = ["reduce", "Broadcast", "matrix_t", "ScalarOp", "activation", "softmax", "gemm",
+from ._lib import (ACT_EXP, ACT_NONE, ACT_RELU, ACT_SIGMOID, ACT_TANH, FN_ABS, FN_COS, FN_ERF,
+                   FN_EXP, FN_INVERSE, FN_LOG, FN_NEG, FN_RCP, FN_RSQRT, FN_SIGN, FN_SIN, FN_SQRT,
+                   FN_SQUARE, OP_ADD, OP_DIV, OP_MAX, OP_MIN, OP_MUL, OP_POW, OP_SUB, call)
+
+__all__ = ["reduce", "Broadcast", "matrix_t", "ScalarOp", "wise", "activation", "softmax", "gemm",
            "train", "Mlp3", "ACT_NONE", "ACT_RELU", "ACT_SIGMOID", "ACT_TANH", "ACT_EXP"]
 
 
@@ -157,6 +160,92 @@ class ScalarOp:
     @staticmethod
     def div(Xx, value, Xz, N, stream=None):
         ScalarOp._run(OP_DIV, Xx, value, Xz, N, stream)
+
+
+class wise:
+    """avx2::wise / nv::ElementWise (Engine/AVX2/wise.hpp:28-42,
+    Engine/CUDA/element_wise.cuh:11-27): Xz = fn(Xx) over N elements (N
+    defaults to Xx.size, the TensorView's element count)."""
+
+    @staticmethod
+    def _fn(fn, Xx, Xz, N, stream):
+        call("cxm_wise_f32", _p(Xx), _p(Xz), Xx.size if N is None else N, fn, _s(stream))
+
+    @staticmethod
+    def square(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_SQUARE, Xx, Xz, N, stream)
+
+    @staticmethod
+    def sqrt(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_SQRT, Xx, Xz, N, stream)
+
+    @staticmethod
+    def rsqrt(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_RSQRT, Xx, Xz, N, stream)
+
+    @staticmethod
+    def log(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_LOG, Xx, Xz, N, stream)
+
+    @staticmethod
+    def exp(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_EXP, Xx, Xz, N, stream)
+
+    @staticmethod
+    def erf(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_ERF, Xx, Xz, N, stream)
+
+    @staticmethod
+    def sin(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_SIN, Xx, Xz, N, stream)
+
+    @staticmethod
+    def cos(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_COS, Xx, Xz, N, stream)
+
+    @staticmethod
+    def abs(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_ABS, Xx, Xz, N, stream)
+
+    @staticmethod
+    def neg(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_NEG, Xx, Xz, N, stream)
+
+    @staticmethod
+    def rcp(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_RCP, Xx, Xz, N, stream)
+
+    @staticmethod
+    def inverse(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_INVERSE, Xx, Xz, N, stream)
+
+    @staticmethod
+    def sign(Xx, Xz, N=None, stream=None):
+        wise._fn(FN_SIGN, Xx, Xz, N, stream)
+
+    @staticmethod
+    def pow(Xx, y, Xz, N=None, stream=None):
+        """pow(Xx, value) when y is a number, else elementwise pow(Xx, Xy)."""
+        n = Xx.size if N is None else N
+        if isinstance(y, (int, float)):
+            call("cxm_scalar_f32", _p(Xx), float(y), _p(Xz), n, OP_POW, _s(stream))
+        else:
+            call("cxm_binary_f32", _p(Xx), _p(y), _p(Xz), n, OP_POW, _s(stream))
+
+    @staticmethod
+    def lerp(Xx, value1, value2, Xz, N, stream=None):
+        call("cxm_lerp_f32", _p(Xx), float(value1), float(value2), _p(Xz), N, _s(stream))
+
+    @staticmethod
+    def clamp(Xx, lo, hi, Xz, N, stream=None):
+        call("cxm_clamp_f32", _p(Xx), float(lo), float(hi), _p(Xz), N, _s(stream))
+
+    @staticmethod
+    def gather(Xx, Xy, Xz, N, x_n=None, stream=None):
+        """Xz[i] = Xx[Xy[i]]; Xx's dtype (float32 or int32) picks the form."""
+        xn = Xx.size if x_n is None else x_n
+        fn = "cxm_gather_i32" if np.dtype(Xx.dtype) == np.int32 else "cxm_gather_f32"
+        call(fn, _p(Xx), xn, _p(Xy), _p(Xz), N, _s(stream))
 
 
 class activation:

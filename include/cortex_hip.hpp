@@ -120,6 +120,47 @@ struct ScalarOp {
     static void div(const float *Xx, float v, float *Xz, std::size_t N) { op(Xx, v, Xz, N, CXM_OP_DIV); }
 };
 
+// avx2::wise / nv::ElementWise (Engine/AVX2/wise.hpp:28-42,
+// Engine/CUDA/element_wise.cuh:11-27) in pointer form: Xz = fn(Xx) over N.
+struct wise {
+    static void fn(const float *Xx, float *Xz, std::size_t N, int code) {
+        check(cxm_wise_f32(Xx, Xz, N, code, stream()), "wise");
+    }
+    static void square(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_SQUARE); }
+    static void sqrt(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_SQRT); }
+    static void rsqrt(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_RSQRT); }
+    static void log(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_LOG); }
+    static void exp(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_EXP); }
+    static void erf(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_ERF); }
+    static void sin(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_SIN); }
+    static void cos(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_COS); }
+    static void abs(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_ABS); }
+    static void neg(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_NEG); }
+    static void rcp(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_RCP); }
+    static void inverse(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_INVERSE); }
+    static void sign(const float *Xx, float *Xz, std::size_t N) { fn(Xx, Xz, N, CXM_FN_SIGN); }
+    static void pow(const float *Xx, float value, float *Xz, std::size_t N) {
+        check(cxm_scalar_f32(Xx, value, Xz, N, CXM_OP_POW, stream()), "wise::pow");
+    }
+    static void pow(const float *Xx, const float *Xy, float *Xz, std::size_t N) {
+        check(cxm_binary_f32(Xx, Xy, Xz, N, CXM_OP_POW, stream()), "wise::pow");
+    }
+    // wise.hpp:44-47 (the gather forms take the size of Xx as well, for bounds)
+    static void lerp(const float *Xx, float value1, float value2, float *Xz, std::size_t N) {
+        check(cxm_lerp_f32(Xx, value1, value2, Xz, N, stream()), "wise::lerp");
+    }
+    static void clamp(const float *Xx, float min, float max, float *Xz, std::size_t N) {
+        check(cxm_clamp_f32(Xx, min, max, Xz, N, stream()), "wise::clamp");
+    }
+    static void gather(const float *Xx, std::size_t Nx, const std::int32_t *Xy, float *Xz, std::size_t N) {
+        check(cxm_gather_f32(Xx, Nx, Xy, Xz, N, stream()), "wise::gather");
+    }
+    static void gather(const std::int32_t *Xx, std::size_t Nx, const std::int32_t *Xy, std::int32_t *Xz,
+                       std::size_t N) {
+        check(cxm_gather_i32(Xx, Nx, Xy, Xz, N, stream()), "wise::gather");
+    }
+};
+
 // Tensor-level forms of avx2::relu / sigmoid / tanh / exp (functions.hpp:
 // 186-188, 372-374, 381-383, 405-411), which the reference has only as
 // 8-lane register functions.

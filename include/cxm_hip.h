@@ -45,6 +45,7 @@ typedef struct ihipEvent_t *cxm_event_t;   /* a hipEvent_t */
 #define CXM_OP_DIV 3
 #define CXM_OP_MAX 4
 #define CXM_OP_MIN 5
+#define CXM_OP_POW 6 /* powf(x, y): same-shape and scalar forms only */
 
 /* Activation codes (Engine/AVX2/functions.hpp:186-188 exp, 372-374 relu,
  * 381-383 tanh, 405-411 sigmoid). */
@@ -53,6 +54,22 @@ typedef struct ihipEvent_t *cxm_event_t;   /* a hipEvent_t */
 #define CXM_ACT_SIGMOID 2
 #define CXM_ACT_TANH 3
 #define CXM_ACT_EXP 4
+
+/* Elementwise math codes for cxm_wise_f32: nv::ElementWise
+ * (Engine/CUDA/element_wise.cuh:11-27) and avx2::wise (Engine/AVX2/wise.hpp:28-42). */
+#define CXM_FN_SQUARE 0
+#define CXM_FN_SQRT 1
+#define CXM_FN_RSQRT 2
+#define CXM_FN_LOG 3
+#define CXM_FN_EXP 4
+#define CXM_FN_ERF 5
+#define CXM_FN_SIN 6
+#define CXM_FN_COS 7
+#define CXM_FN_ABS 8
+#define CXM_FN_NEG 9
+#define CXM_FN_RCP 10
+#define CXM_FN_INVERSE 11
+#define CXM_FN_SIGN 12
 
 /* Human-readable text for a status code (never NULL). */
 const char *cxm_error_string(int status);
@@ -114,7 +131,9 @@ int cxm_reduce_argmax_f32(const float *x, int32_t *z, size_t outer, size_t dim, 
  * Same-shape binary z = x op y: matrix_t::{add,sub,mul,div,max,min}
  * (Engine/AVX2/matrix.hpp:38-94) and nv::Matrix (Engine/CUDA/matrix.cuh:12-25).
  * z may alias x (the in-place forms, matrix.hpp:130-160).  max/min are
- * (x > y ? x : y) / (x < y ? x : y), as _mm256_max_ps / _mm256_min_ps. */
+ * (x > y ? x : y) / (x < y ? x : y), as _mm256_max_ps / _mm256_min_ps.
+ * CXM_OP_POW is powf(x, y): nv::ElementWise::pow(Xx, Xy, Xz)
+ * (Engine/CUDA/element_wise.cu:39-49; ops::Power, Operations/kernel_ops.cuh:88-100). */
 int cxm_binary_f32(const float *x, const float *y, float *z, size_t n, int op, cxm_stream_t s);
 /* Row broadcast z[i,j] = x[i,j] op y[j] over [m, n]: Broadcast::row
  * (Engine/AVX2/broadcast.hpp:28-37).  Column broadcast z[i,j] = x[i,j] op y[i]:
@@ -124,12 +143,37 @@ int cxm_bcast_row_f32(const float *x, const float *y, float *z, size_t m, size_t
 int cxm_bcast_col_f32(const float *x, const float *y, float *z, size_t m, size_t n, int op,
                       cxm_stream_t s);
 /* Tensor-op-scalar z = x op value: ScalarOp (Engine/AVX2/scalar.cpp:89-119),
- * nv::ScalarKernel (Engine/CUDA/scalar.cu:16-134).  z may alias x. */
+ * nv::ScalarKernel (Engine/CUDA/scalar.cu:16-134).  z may alias x.
+ * CXM_OP_POW is powf(x, value): nv::ElementWise::pow(Xx, value, Xz)
+ * (Engine/CUDA/element_wise.cu:28-37) and avx2::wise::pow (Engine/AVX2/wise.cpp:60-91). */
 int cxm_scalar_f32(const float *x, float value, float *z, size_t n, int op, cxm_stream_t s);
 /* z = act(x) for act in RELU, SIGMOID, TANH, EXP (Engine/AVX2/functions.hpp:
  * 372-374, 405-411, 381-383, 186-188; nv::ElementWise::exp,
- * Engine/CUDA/element_wise.cu:84-92).  relu(x) = (0 > x) ? 0 : x. */
+ * Engine/CUDA/element_wise.cu:84-93).  relu(x) = (0 > x) ? 0 : x. */
 int cxm_unary_f32(const float *x, float *z, size_t n, int act, cxm_stream_t s);
+/* z = fn(x) for fn in CXM_FN_*: nv::ElementWise::{square, sqrt, rsqrt, log,
+ * exp, erf, sin, cos, abs, neg, rcp, inverse, sign} (Engine/CUDA/element_wise.cu:
+ * 17-181; ops in Operations/kernel_ops.cuh:73-284) and avx2::wise
+ * (Engine/AVX2/wise.cpp:56-143).  z may alias x.  Results: square, abs, neg,
+ * sign exact; sqrt, rcp (= inverse = 1/x) correctly rounded; rsqrt, log, exp,
+ * erf, sin, cos within 2 ulp of the exact value.  sign(x) = (x > 0) - (x < 0),
+ * so sign(NaN) = sign(-0) = +0. */
+int cxm_wise_f32(const float *x, float *z, size_t n, int fn, cxm_stream_t s);
+/* z = fma(v2, v1 - x, x), i.e. x + v2*(v1 - x) with the product and the sum
+ * rounded once: avx2::wise::lerp (Engine/AVX2/wise.cpp:145-155,
+ * functions.hpp:271-274). */
+int cxm_lerp_f32(const float *x, float v1, float v2, float *z, size_t n, cxm_stream_t s);
+/* z = min(max(x, lo), hi) with _mm256_max_ps / _mm256_min_ps operand rules:
+ * avx2::wise::clamp (Engine/AVX2/wise.cpp:157-167, functions.hpp:332-335).
+ * A NaN x gives lo. */
+int cxm_clamp_f32(const float *x, float lo, float hi, float *z, size_t n, cxm_stream_t s);
+/* z[i] = x[idx[i]] for i < n: avx2::wise::gather (Engine/AVX2/wise.cpp:169-194).
+ * x holds x_n elements; an index outside [0, x_n) yields NaN (f32) or
+ * INT32_MIN (i32) instead of reading out of bounds. */
+int cxm_gather_f32(const float *x, size_t x_n, const int32_t *idx, float *z, size_t n,
+                   cxm_stream_t s);
+int cxm_gather_i32(const int32_t *x, size_t x_n, const int32_t *idx, int32_t *z, size_t n,
+                   cxm_stream_t s);
 
 /* Fused y = act(x * scale[j] + bias[j]) over [m, n]: Broadcast::row::mul then
  * Broadcast::row::add in place (broadcast.cpp:206-216, 230-240), then the

@@ -209,7 +209,7 @@ void orc_reduce_argmax(const float *x, int32_t *z, size_t outer, size_t dim, siz
 
 /* ---------------------------------------------------- elementwise binary */
 
-enum { ORC_ADD = 0, ORC_SUB = 1, ORC_MUL = 2, ORC_DIV = 3, ORC_MAX = 4, ORC_MIN = 5 };
+enum { ORC_ADD = 0, ORC_SUB = 1, ORC_MUL = 2, ORC_DIV = 3, ORC_MAX = 4, ORC_MIN = 5, ORC_POW = 6 };
 
 static inline float bin_op(int op, float a, float b) {
     switch (op) {
@@ -218,7 +218,8 @@ static inline float bin_op(int op, float a, float b) {
         case ORC_MUL: return a * b;
         case ORC_DIV: return a / b;
         case ORC_MAX: return simd_max(a, b);     /* _mm256_max_ps(x, y) */
-        default:      return a < b ? a : b;      /* _mm256_min_ps(x, y) */
+        case ORC_MIN: return a < b ? a : b;      /* _mm256_min_ps(x, y) */
+        default:      return powf(a, b);         /* ops::Power, Operations/kernel_ops.hpp:69-78 */
     }
 }
 
@@ -248,6 +249,79 @@ void orc_bcast_col(const float *x, const float *y, float *z, size_t m, size_t n,
  * oracle applies the op to every element, the documented intent. */
 void orc_scalar(const float *x, float value, float *z, size_t n, int op) {
     for (size_t i = 0; i < n; ++i) z[i] = bin_op(op, x[i], value);
+}
+
+/* ------------------------------------------------------ elementwise math */
+
+enum {
+    ORC_FN_SQUARE = 0, ORC_FN_SQRT, ORC_FN_RSQRT, ORC_FN_LOG, ORC_FN_EXP, ORC_FN_ERF, ORC_FN_SIN,
+    ORC_FN_COS, ORC_FN_ABS, ORC_FN_NEG, ORC_FN_RCP, ORC_FN_INVERSE, ORC_FN_SIGN
+};
+
+/* avx2::wise::{square, sqrt, ..., sign} (Engine/AVX2/wise.cpp:56-143) through
+ * kernels::Unary with the scalar operators of Operations/kernel_ops.hpp:58-210:
+ * square x*x (:65), sqrt (:87), rsqrt 1/sqrt(x) (:98), log (:109), exp (:120),
+ * erf (:131), sin (:142), cos (:153), abs (:164), neg (:175), rcp 1/x (:186),
+ * inverse 1/x (:208).  sign follows avx2::sign (functions.hpp:342-355): 1 where
+ * x > 0, -1 where x < 0 (ordered compares), else +0; the scalar tail's
+ * tlx::sign is parity unpinned (TLX absent).  Deviations: the SIMD body of
+ * rcp and rsqrt uses the 12-bit _mm256_rcp_ps / _mm256_rsqrt_ps
+ * (functions.hpp:168-170, 240-242); the oracle uses the exact expressions of
+ * the scalar operators (the CUDA path's __frcp_rn is also exact).  log, exp,
+ * erf, sin and cos call glibc (the reference calls SVML, absent here). */
+static inline float wise_fn(int fn, float x) {
+    switch (fn) {
+        case ORC_FN_SQUARE: return x * x;
+        case ORC_FN_SQRT: return sqrtf(x);
+        case ORC_FN_RSQRT: return 1.0f / sqrtf(x);
+        case ORC_FN_LOG: return logf(x);
+        case ORC_FN_EXP: return expf(x);
+        case ORC_FN_ERF: return erff(x);
+        case ORC_FN_SIN: return sinf(x);
+        case ORC_FN_COS: return cosf(x);
+        case ORC_FN_ABS: return fabsf(x);
+        case ORC_FN_NEG: return -x;
+        case ORC_FN_RCP:
+        case ORC_FN_INVERSE: return 1.0f / x;
+        default: return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
+    }
+}
+
+void orc_wise(const float *x, float *z, size_t n, int fn) {
+    for (size_t i = 0; i < n; ++i) z[i] = wise_fn(fn, x[i]);
+}
+
+/* avx2::wise::lerp (Engine/AVX2/wise.cpp:145-155): fma::add(t, sub(b, a), a)
+ * (functions.hpp:271-274) with a = x, b = value1, t = value2: one rounding
+ * for v1 - x, one for the fused multiply-add. */
+void orc_lerp(const float *x, float v1, float v2, float *z, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        const float d = v1 - x[i];
+        z[i] = fmaf(v2, d, x[i]);
+    }
+}
+
+/* avx2::wise::clamp (Engine/AVX2/wise.cpp:157-167): min(max(x, lo), hi) with
+ * _mm256_max_ps / _mm256_min_ps (functions.hpp:332-335); a NaN x gives lo.
+ * The scalar tail's std::clamp (NaN stays NaN) is not followed. */
+void orc_clamp(const float *x, float lo, float hi, float *z, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        const float m = simd_max(x[i], lo);
+        z[i] = m < hi ? m : hi;
+    }
+}
+
+/* avx2::wise::gather (Engine/AVX2/wise.cpp:169-194): z[i] = x[idx[i]].  The
+ * reference reads out of bounds for a bad index; here such an index gives
+ * NaN (f32) or INT32_MIN (i32). */
+void orc_gather_f32(const float *x, size_t xn, const int32_t *idx, float *z, size_t n) {
+    for (size_t i = 0; i < n; ++i)
+        z[i] = (idx[i] >= 0 && (size_t)idx[i] < xn) ? x[idx[i]] : NAN;
+}
+
+void orc_gather_i32(const int32_t *x, size_t xn, const int32_t *idx, int32_t *z, size_t n) {
+    for (size_t i = 0; i < n; ++i)
+        z[i] = (idx[i] >= 0 && (size_t)idx[i] < xn) ? x[idx[i]] : INT32_MIN;
 }
 
 /* ----------------------------------------------------------- activations */

@@ -19,7 +19,9 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libcxm_oracle.so")
 
-ADD, SUB, MUL, DIV, MAX, MIN = range(6)
+ADD, SUB, MUL, DIV, MAX, MIN, POW = range(7)
+(FN_SQUARE, FN_SQRT, FN_RSQRT, FN_LOG, FN_EXP, FN_ERF, FN_SIN, FN_COS, FN_ABS, FN_NEG, FN_RCP,
+ FN_INVERSE, FN_SIGN) = range(13)
 ACT_NONE, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_EXP = range(5)
 
 _F = ctypes.POINTER(ctypes.c_float)
@@ -57,6 +59,11 @@ def lib() -> ctypes.CDLL:
             "orc_bcast_col": [_F, _F, _F, _SZ, _SZ, ctypes.c_int],
             "orc_scalar": [_F, ctypes.c_float, _F, _SZ, ctypes.c_int],
             "orc_unary": [_F, _F, _SZ, ctypes.c_int],
+            "orc_wise": [_F, _F, _SZ, ctypes.c_int],
+            "orc_lerp": [_F, ctypes.c_float, ctypes.c_float, _F, _SZ],
+            "orc_clamp": [_F, ctypes.c_float, ctypes.c_float, _F, _SZ],
+            "orc_gather_f32": [_F, _SZ, _I, _F, _SZ],
+            "orc_gather_i32": [_I, _SZ, _I, _I, _SZ],
             "orc_affine_act_fwd": [_F, _F, _F, _F, _SZ, _SZ, ctypes.c_int],
             "orc_affine_act_bwd": [_F, _F, _F, _F, _F, _F, _F, _SZ, _SZ, ctypes.c_int],
             "orc_softmax_fwd": [_F, _F, _SZ, _SZ, ctypes.c_int],
@@ -151,6 +158,40 @@ def unary(x, act: int) -> np.ndarray:
     x = _c32(x)
     z = np.empty_like(x)
     lib().orc_unary(_f(x), _f(z), x.size, act)
+    return z
+
+
+def wise(x, fn: int) -> np.ndarray:
+    x = _c32(x)
+    z = np.empty_like(x)
+    lib().orc_wise(_f(x), _f(z), x.size, fn)
+    return z
+
+
+def lerp(x, v1: float, v2: float) -> np.ndarray:
+    x = _c32(x)
+    z = np.empty_like(x)
+    lib().orc_lerp(_f(x), float(v1), float(v2), _f(z), x.size)
+    return z
+
+
+def clamp(x, lo: float, hi: float) -> np.ndarray:
+    x = _c32(x)
+    z = np.empty_like(x)
+    lib().orc_clamp(_f(x), float(lo), float(hi), _f(z), x.size)
+    return z
+
+
+def gather(x, idx) -> np.ndarray:
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    if np.asarray(x).dtype == np.int32:
+        x = np.ascontiguousarray(x, dtype=np.int32)
+        z = np.empty(idx.size, np.int32)
+        lib().orc_gather_i32(_i(x), x.size, _i(idx), _i(z), idx.size)
+        return z
+    x = _c32(x)
+    z = np.empty(idx.size, np.float32)
+    lib().orc_gather_f32(_f(x), x.size, _i(idx), _f(z), idx.size)
     return z
 
 

@@ -103,6 +103,28 @@ int main() {
             EXPECT(hC[i * N + j] == s, "matmul %zu,%zu", i, j);
         }
 
+    // wise::square / abs / sign and the pow and gather forms on small integers (exact)
+    std::vector<float> w(1000);
+    for (size_t i = 0; i < w.size(); ++i) w[i] = static_cast<float>(static_cast<int>(i % 23) - 11);
+    Dev<float> dw(w), dq(w.size()), dp(w.size()), ds(w.size());
+    hip::wise::square(dw.p, dq.p, w.size());
+    hip::wise::pow(dw.p, 3.0f, dp.p, w.size());
+    hip::wise::sign(dw.p, ds.p, w.size());
+    std::vector<int32_t> gi(500);
+    for (size_t i = 0; i < gi.size(); ++i) gi[i] = static_cast<int32_t>((i * 37) % w.size());
+    Dev<int32_t> dgi(gi);
+    Dev<float> dg(gi.size());
+    hip::wise::gather(dw.p, w.size(), dgi.p, dg.p, gi.size());
+    auto hq = dq.get(), hp = dp.get(), hs = ds.get(), hg = dg.get();
+    for (size_t i = 0; i < w.size(); ++i) {
+        EXPECT(hq[i] == w[i] * w[i], "square %zu", i);
+        const float cube = w[i] * w[i] * w[i];  // exact for these integers
+        EXPECT(std::fabs(hp[i] - cube) <= 2.4e-7f * std::fabs(cube), "pow %zu: %f", i, hp[i]);
+        EXPECT(hs[i] == static_cast<float>((w[i] > 0) - (w[i] < 0)), "sign %zu", i);
+        if (failures > 10) break;
+    }
+    for (size_t i = 0; i < gi.size(); ++i) EXPECT(hg[i] == w[gi[i]], "gather %zu", i);
+
     if (failures == 0) std::printf("ALL OK\n");
     return failures == 0 ? 0 : 1;
 }

@@ -336,3 +336,118 @@ def test_mlp_two_steps_vs_torch(orc):
     for k, v in params.items():
         ref = FIX[f"mlp_final_{k}"]
         assert np.allclose(v, ref, rtol=1e-4, atol=1e-6), k
+
+
+# ------------------------------------------------------- elementwise math
+
+def _round_f32(fr):
+    """Nearest float32 to an exact rational (ties to even)."""
+    from fractions import Fraction
+    c = np.float32(float(fr))
+    best = None
+    for cand in (np.nextafter(c, np.float32(-np.inf)), c, np.nextafter(c, np.float32(np.inf))):
+        d = abs(Fraction(float(cand)) - fr)
+        key = (d, int(np.float32(cand).view(np.uint32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, cand)
+    return np.float32(best[1])
+
+
+def test_wise_exact_ops_vs_numpy(orc):
+    # square/abs/neg are exact or single-rounded; numpy float32 ufuncs are IEEE.
+    rng = np.random.default_rng(41)
+    x = np.concatenate([rng.normal(0, 1e3, 5000), [0.0, -0.0, np.inf, -np.inf, 3e19, -3e19]]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(orc.wise(x, orc.FN_SQUARE).view(np.uint32), np.square(x).view(np.uint32))
+    assert np.array_equal(orc.wise(x, orc.FN_ABS).view(np.uint32), np.abs(x).view(np.uint32))
+    assert np.array_equal(orc.wise(x, orc.FN_NEG).view(np.uint32), np.negative(x).view(np.uint32))
+
+
+def test_wise_correctly_rounded_ops_vs_numpy(orc):
+    # sqrt and 1/x are correctly rounded in IEEE arithmetic (numpy float32)
+    rng = np.random.default_rng(42)
+    x = np.abs(rng.normal(0, 50, 20000)).astype(np.float32) + np.float32(1e-30)
+    assert np.array_equal(orc.wise(x, orc.FN_SQRT), np.sqrt(x))
+    y = np.concatenate([x, -x]).astype(np.float32)
+    assert np.array_equal(orc.wise(y, orc.FN_RCP), np.float32(1.0) / y)
+    assert np.array_equal(orc.wise(y, orc.FN_INVERSE), np.float32(1.0) / y)
+    # rsqrt = 1/sqrt(x): two correctly rounded steps stay within 1 ulp of exact
+    exact = (1.0 / np.sqrt(x.astype(np.float64))).astype(np.float32)
+    assert ulp_dist(orc.wise(x, orc.FN_RSQRT), exact).max() <= 1
+
+
+def test_wise_sign_table(orc):
+    x = f32([3.5, -2.0, 0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45])
+    z = orc.wise(x, orc.FN_SIGN)
+    assert z.tolist()[:6] == [1.0, -1.0, 0.0, 0.0, 1.0, -1.0]
+    assert z[6] == 0.0 and not np.signbit(z[6])  # ordered compares: NaN -> +0
+    assert not np.signbit(z[3])  # sign(-0) = +0
+    assert z[7] == 1.0 and z[8] == -1.0  # denormals keep their sign
+    v = np.random.default_rng(43).normal(size=1000).astype(np.float32)
+    assert np.array_equal(orc.wise(v, orc.FN_SIGN), np.sign(v))
+
+
+@pytest.mark.parametrize("fn,lo,hi,ref", [
+    ("FN_LOG", 1e-30, 1e30, np.log), ("FN_EXP", -87.0, 88.0, np.exp),
+    ("FN_SIN", -100.0, 100.0, np.sin), ("FN_COS", -100.0, 100.0, np.cos),
+    ("FN_ERF", -6.0, 6.0, None)])
+def test_wise_transcendentals_within_1ulp_of_float64(orc, fn, lo, hi, ref):
+    import scipy.special
+    rng = np.random.default_rng(44)
+    if fn == "FN_LOG":
+        x = np.exp(rng.uniform(np.log(lo), np.log(hi), 50000)).astype(np.float32)
+    else:
+        x = rng.uniform(lo, hi, 50000).astype(np.float32)
+    f = scipy.special.erf if ref is None else ref
+    exact = f(x.astype(np.float64)).astype(np.float32)
+    assert ulp_dist(orc.wise(x, getattr(orc, fn)), exact).max() <= 1
+
+
+def test_pow_vs_float64(orc):
+    rng = np.random.default_rng(45)
+    x = rng.uniform(0.01, 10, 20000).astype(np.float32)
+    y = rng.uniform(-6, 6, 20000).astype(np.float32)
+    exact = np.power(x.astype(np.float64), y.astype(np.float64)).astype(np.float32)
+    assert ulp_dist(orc.binary(x, y, orc.POW), exact).max() <= 1
+    e2 = np.power(x.astype(np.float64), np.float64(np.float32(2.5))).astype(np.float32)
+    assert ulp_dist(orc.scalar(x, 2.5, orc.POW), e2).max() <= 1
+    # IEEE special cases of pow
+    sx = f32([-2.0, -2.0, 0.0, 1.0, 5.0, np.nan])
+    sy = f32([3.0, 0.5, -1.0, np.nan, 0.0, 0.0])
+    z = orc.binary(sx, sy, orc.POW)
+    assert z[0] == -8.0 and np.isnan(z[1]) and z[2] == np.inf and z[3] == 1.0 and z[4] == 1.0 and z[5] == 1.0
+
+
+def test_lerp_single_fma_rounding(orc):
+    # exact rational x + v2*(v1 - x) with (v1 - x) rounded to float32 first,
+    # rounded once: a two-rounding mul+add or an unrounded difference fails
+    from fractions import Fraction
+    rng = np.random.default_rng(46)
+    x = rng.normal(0, 10, 600).astype(np.float32)
+    v1, v2 = np.float32(3.3), np.float32(0.7)
+    z = orc.lerp(x, v1, v2)
+    d = (v1 - x).astype(np.float32)
+    for i in range(x.size):
+        exact = Fraction(float(v2)) * Fraction(float(d[i])) + Fraction(float(x[i]))
+        assert z[i] == _round_f32(exact), i
+
+
+def test_clamp_vs_numpy_clip(orc):
+    rng = np.random.default_rng(47)
+    x = rng.normal(0, 3, 10000).astype(np.float32)
+    assert np.array_equal(orc.clamp(x, -1.5, 2.0), np.clip(x, np.float32(-1.5), np.float32(2.0)))
+    z = orc.clamp(f32([np.nan, -np.inf, np.inf]), -1.0, 1.0)
+    assert z.tolist() == [-1.0, -1.0, 1.0]  # _mm256_max_ps(NaN, lo) = lo
+
+
+def test_gather_vs_numpy_indexing(orc):
+    rng = np.random.default_rng(48)
+    x = rng.normal(size=1000).astype(np.float32)
+    xi = rng.integers(-1000, 1000, 1000).astype(np.int32)
+    idx = rng.integers(0, 1000, 5000).astype(np.int32)
+    assert np.array_equal(orc.gather(x, idx), x[idx])
+    assert np.array_equal(orc.gather(xi, idx), xi[idx])
+    bad = np.array([-1, 1000, 5], np.int32)
+    zf, zi = orc.gather(x, bad), orc.gather(xi, bad)
+    assert np.isnan(zf[0]) and np.isnan(zf[1]) and zf[2] == x[5]
+    assert zi.tolist() == [-(2 ** 31), -(2 ** 31), xi[5]]
