@@ -23,8 +23,10 @@ profiles/pmc_traffic.txt when that file has a line for the kernel.
 over a bounded sample of whole steps.
 
 The default run also reports the other workloads (C1 softmax, C3 affine
-fwd/bwd, C4 long-row softmax fwd/bwd, C5 MLP training step) under
-"workloads"; --workload cN makes one of them the headline, for profiling.
+fwd/bwd, C4 long-row softmax fwd/bwd, C5 MLP training step, and "more":
+the rest of the reduction and elementwise-math surface at the C2/C3
+shapes) under "workloads"; --workload NAME makes one of them the headline,
+for profiling.
 """
 from __future__ import annotations
 
@@ -50,7 +52,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    p.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "more"])
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip the other workloads")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -127,7 +129,7 @@ def wl_c3(E, D):
     big = 4 * m * n
     ops = []
     for act, nm in [(E.ACT_RELU, "relu"), (E.ACT_SIGMOID, "sigmoid"), (E.ACT_TANH, "tanh")]:
-        ops.append(Op(f"fwd_{nm}", f"k_affine_fwd_vec<{nm}>",
+        ops.append(Op(f"fwd_{nm}", f"k_rowmap4<AffineF<{nm}>>",
                       lambda k, act=act: A.affine_fwd(dx_, ds_, db_, y_, m, n, act), 2 * big + 2 * 4 * n))
     for act, nm in [(E.ACT_RELU, "relu"), (E.ACT_SIGMOID, "sigmoid"), (E.ACT_TANH, "tanh")]:
         ops.append(Op(f"bwd_{nm}", f"k_affine_bwd<{nm}>",
@@ -182,7 +184,54 @@ def wl_c5(E, D):
     return ops, desc, (dx_, dl_, P, loss, net, h1, h2, gemm_op), None
 
 
-WORKLOADS = {"c1": wl_c1, "c2": wl_c2, "c3": wl_c3, "c4": wl_c4, "c5": wl_c5}
+def wl_more(E, D):
+    """The rest of the operator surface at the C2 / C3 shapes: min, argmin,
+    norm1, norm2, var, stdv on fp32 [4096, 4096] (global, axis 1, axis 0),
+    and elementwise math on fp32 [8192, 8192] (1 read + 1 write each; pow
+    with a tensor exponent reads two)."""
+    from cortexmind_amd.data import c2_reduce, c3_affine
+
+    x = c2_reduce()
+    rows, cols = x.shape
+    n = x.size
+    nbuf = 10
+    bufs = [D.from_numpy(x) for _ in range(nbuf)]
+    z1, zf, zi = D((1,), np.float32), D((4096,), np.float32), D((4096,), np.int32)
+    xb = 4 * n
+    R = E.reduce
+
+    def rot(f):
+        return lambda k: f(bufs[k % nbuf])
+
+    ops = []
+    for op in ("min", "argmin", "norm1", "norm2", "var", "stdv"):
+        z = zi if op == "argmin" else zf
+        fn = getattr(R, op)
+        kern = {"min": "MinOp", "argmin": "ArgMinOp", "norm1": "AbsSumOp", "norm2": "SqSumOp",
+                "var": "Pow2Op", "stdv": "Pow2Op"}[op]
+        ops.append(Op(f"{op}_global", f"k_rows<{kern}>", rot(lambda b, fn=fn: fn(b, z1, n)), xb + 4))
+        ops.append(Op(f"{op}_axis1", f"k_rows<{kern}>", rot(lambda b, fn=fn, z=z: fn(b, z, rows, cols, 1)),
+                      xb + 4 * rows))
+        ops.append(Op(f"{op}_axis0", f"k_cols<{kern}>", rot(lambda b, fn=fn, z=z: fn(b, z, 1, rows, cols)),
+                      xb + 4 * cols))
+    X = c3_affine()[0]
+    big = X.size
+    xs = [D.from_numpy(X) for _ in range(2)]
+    ys = [D((big,), np.float32) for _ in range(2)]
+    W = E.wise
+    for nm in ("sqrt", "exp", "sin", "erf"):
+        f = getattr(W, nm)
+        ops.append(Op(f"wise_{nm}", "k_map4", lambda k, f=f: f(xs[k % 2], ys[k % 2], big), 8 * big))
+    ops.append(Op("wise_pow_scalar", "k_map4<ScalarF<POW>>", lambda k: W.pow(xs[k % 2], 2.5, ys[k % 2], big), 8 * big))
+    ops.append(Op("wise_pow_tensor", "k_zip4<BinF<POW>>", lambda k: W.pow(xs[k % 2], xs[(k + 1) % 2], ys[k % 2], big),
+                  12 * big))
+    ops.append(Op("wise_lerp", "k_map4", lambda k: W.lerp(xs[k % 2], 3.0, 0.25, ys[k % 2], big), 8 * big))
+    desc = {"workload": "reductions min/argmin/norm1/norm2/var/stdv on fp32 [4096,4096] and elementwise "
+                        "math on fp32 [8192,8192]", "ops": [o.name for o in ops]}
+    return ops, desc, (bufs, z1, zf, zi, xs, ys), x
+
+
+WORKLOADS = {"c1": wl_c1, "c2": wl_c2, "c3": wl_c3, "c4": wl_c4, "c5": wl_c5, "more": wl_more}
 
 
 # ------------------------------------------------------------------ timing
@@ -356,7 +405,7 @@ def main():
         out["cpu_baseline"] = cpu_c2(head["host"], args.cpu_seconds)
     if not args.no_extra:
         wl = {}
-        for name in [w for w in ["c1", "c3", "c4", "c5"] if w != args.workload]:
+        for name in [w for w in ["c1", "c3", "c4", "c5", "more"] if w != args.workload]:
             r = run_workload(name, max(5, args.steps // 5), 2, E, D, Event, sync)
             wl[name] = {"workload": r["config"]["workload"], "value": round(r["value"], 2),
                         "unit": r["unit"], "ms_per_step": round(r["ms_per_step"], 5),

@@ -60,6 +60,18 @@ SIGNATURES = {
     "cxm_reduce_mean_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
     "cxm_reduce_max_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
     "cxm_reduce_argmax_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
+    "cxm_reduce_min_flat_f32": [_P, _P, _SZ, _P],
+    "cxm_reduce_min_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
+    "cxm_reduce_argmin_flat_f32": [_P, _P, _SZ, _P],
+    "cxm_reduce_argmin_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
+    "cxm_reduce_norm1_flat_f32": [_P, _P, _SZ, _P],
+    "cxm_reduce_norm1_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
+    "cxm_reduce_norm2_flat_f32": [_P, _P, _SZ, _P],
+    "cxm_reduce_norm2_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
+    "cxm_reduce_var_flat_f32": [_P, _P, _SZ, _P],
+    "cxm_reduce_var_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
+    "cxm_reduce_stdv_flat_f32": [_P, _P, _SZ, _P],
+    "cxm_reduce_stdv_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
     "cxm_binary_f32": [_P, _P, _P, _SZ, _I, _P],
     "cxm_bcast_row_f32": [_P, _P, _P, _SZ, _SZ, _I, _P],
     "cxm_bcast_col_f32": [_P, _P, _P, _SZ, _SZ, _I, _P],

@@ -1,12 +1,15 @@
-// Elementwise fp32 kernels: same-shape binary ops (pow included), row/column broadcast,
-// tensor-op-scalar, unary activations, the fused affine + activation
-// forward/backward of the C3 workload, and the SGD update.
+// Elementwise fp32 kernels: same-shape binary ops (pow included), row/column
+// broadcast, tensor-op-scalar, unary activations, the fused affine +
+// activation forward/backward of the C3 workload, and the SGD update.
 //
 // Replaces the float4 grid-stride loops of the reference's CUDA path
 // (kernels::Binary / kernels::scalar / kernels::Unary,
 // source/CortexMind/framework/Engine/Kernels/binary.cuh:15-39,
 // scalar.cuh:30-54, unary.cuh:16-40) and the CPU Broadcast::row/col
-// (Engine/AVX2/broadcast.cpp:182-388), which has no GPU form there.
+// (Engine/AVX2/broadcast.cpp:182-388), which has no GPU form there.  The
+// aligned forms run as the one-float4-per-thread streaming maps of
+// cxm_common.hpp (k_map4, k_zip4, k_rowmap4) with the functors below;
+// unaligned pointers take scalar grid-stride loops.
 //
 // Every op rounds exactly as the reference's scalar expression does: the
 // library is built with -ffp-contract=off, so x*s+b is a rounded product
@@ -89,21 +92,6 @@ inline unsigned stream_grid(size_t n4) {
 
 // -------------------------------------------------------------- binary
 
-template <int OP>
-__global__ __launch_bounds__(kBlock) void k_binary_vec(const float *__restrict__ x,
-                                                       const float *__restrict__ y, float *z,
-                                                       size_t n) {
-    const size_t n4 = n / 4;
-    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride)
-        st4(z + 4 * i, bin4<OP>(ld4(x + 4 * i), ld4(y + 4 * i)));
-    // tail (n % 4 elements) by the first threads of block 0
-    if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
-        const size_t j = 4 * n4 + threadIdx.x;
-        z[j] = bin_t<OP>(x[j], y[j]);
-    }
-}
-
 __global__ __launch_bounds__(kBlock) void k_binary_scalar(const float *x, const float *y, float *z,
                                                           size_t n, int op) {
     const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
@@ -112,40 +100,6 @@ __global__ __launch_bounds__(kBlock) void k_binary_scalar(const float *x, const 
 }
 
 // ------------------------------------------------------------ broadcast
-
-// Row broadcast z[i,j] = x[i,j] op y[j], n % 4 == 0: a thread keeps one
-// float4 of y and walks rows.  grid.x = column tiles of 256 float4, grid.y
-// = row chunks.
-template <int OP>
-__global__ __launch_bounds__(kBlock) void k_bcast_row_vec(const float *x, const float *__restrict__ y,
-                                                          float *z, size_t m, size_t n,
-                                                          size_t rows_per_chunk) {
-    const size_t j4 = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (4 * j4 >= n) return;
-    const float4 yv = ld4(y + 4 * j4);
-    const size_t r0 = static_cast<size_t>(blockIdx.y) * rows_per_chunk;
-    const size_t r1 = r0 + rows_per_chunk < m ? r0 + rows_per_chunk : m;
-    for (size_t r = r0; r < r1; ++r) {
-        const size_t o = r * n + 4 * j4;
-        st4(z + o, bin4<OP>(ld4(x + o), yv));
-    }
-}
-
-// Column broadcast z[i,j] = x[i,j] op y[i], n % 4 == 0.
-template <int OP>
-__global__ __launch_bounds__(kBlock) void k_bcast_col_vec(const float *x, const float *__restrict__ y,
-                                                          float *z, size_t m, size_t n,
-                                                          size_t rows_per_chunk) {
-    const size_t j4 = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (4 * j4 >= n) return;
-    const size_t r0 = static_cast<size_t>(blockIdx.y) * rows_per_chunk;
-    const size_t r1 = r0 + rows_per_chunk < m ? r0 + rows_per_chunk : m;
-    for (size_t r = r0; r < r1; ++r) {
-        const float v = y[r];
-        const size_t o = r * n + 4 * j4;
-        st4(z + o, bin4<OP>(ld4(x + o), make_float4(v, v, v, v)));
-    }
-}
 
 __global__ __launch_bounds__(kBlock) void k_bcast_scalar(const float *x, const float *y, float *z,
                                                          size_t m, size_t n, int op, int row_mode) {
@@ -160,19 +114,6 @@ __global__ __launch_bounds__(kBlock) void k_bcast_scalar(const float *x, const f
 
 // --------------------------------------------------------------- scalar
 
-template <int OP>
-__global__ __launch_bounds__(kBlock) void k_scalar_vec(const float *x, float v, float *z, size_t n) {
-    const size_t n4 = n / 4;
-    const float4 vv = make_float4(v, v, v, v);
-    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride)
-        st4(z + 4 * i, bin4<OP>(ld4(x + 4 * i), vv));
-    if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
-        const size_t j = 4 * n4 + threadIdx.x;
-        z[j] = bin_t<OP>(x[j], v);
-    }
-}
-
 __global__ __launch_bounds__(kBlock) void k_scalar_scalar(const float *x, float v, float *z, size_t n,
                                                           int op) {
     const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
@@ -182,59 +123,64 @@ __global__ __launch_bounds__(kBlock) void k_scalar_scalar(const float *x, float 
 
 // ---------------------------------------------------------------- unary
 
-template <int ACT, bool VEC>
-__global__ __launch_bounds__(kBlock) void k_unary(const float *x, float *z, size_t n) {
+template <int ACT>
+__global__ __launch_bounds__(kBlock) void k_unary_scalar(const float *x, float *z, size_t n) {
     const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-    size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if constexpr (VEC) {
-        const size_t n4 = n / 4;
-        for (; i < n4; i += stride) st4(z + 4 * i, act4<ACT>(ld4(x + 4 * i)));
-        if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
-            const size_t j = 4 * n4 + threadIdx.x;
-            z[j] = act<ACT>(x[j]);
-        }
-    } else {
-        for (; i < n; i += stride) z[i] = act<ACT>(x[i]);
-    }
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+        z[i] = act<ACT>(x[i]);
 }
+
+// Functors of the streaming maps (k_map4 / k_zip4 / k_rowmap4).
+template <int OP>
+struct BinF {
+    __device__ float operator()(float a, float b) const { return bin_t<OP>(a, b); }
+};
+template <int OP>
+struct ScalarF {
+    float v;
+    __device__ float operator()(float a) const { return bin_t<OP>(a, v); }
+};
+template <int ACT>
+struct ActF {
+    __device__ float operator()(float t) const { return act<ACT>(t); }
+};
+// z[i,j] = x[i,j] op y[j]
+template <int OP>
+struct RowBcastF {
+    const float *y;
+    __device__ float4 operator()(float4 v, unsigned, size_t j4) const { return bin4<OP>(v, ld4(y + 4 * j4)); }
+};
+// z[i,j] = x[i,j] op y[i]
+template <int OP>
+struct ColBcastF {
+    const float *y;
+    __device__ float4 operator()(float4 v, unsigned row, size_t) const {
+        const float c = y[row];
+        return bin4<OP>(v, make_float4(c, c, c, c));
+    }
+};
+// y = act(x*scale[j] + bias[j]): product and sum rounded separately
+template <int ACT>
+struct AffineF {
+    const float *scale, *bias;
+    __device__ float4 operator()(float4 v, unsigned, size_t j4) const {
+        const float4 sc = ld4(scale + 4 * j4), b = ld4(bias + 4 * j4);
+        float4 t;
+        t.x = v.x * sc.x; t.y = v.y * sc.y; t.z = v.z * sc.z; t.w = v.w * sc.w;
+        t.x = t.x + b.x; t.y = t.y + b.y; t.z = t.z + b.z; t.w = t.w + b.w;
+        return act4<ACT>(t);
+    }
+};
+// w - g*lr, two roundings
+struct SgdF {
+    float lr;
+    __device__ float operator()(float w, float g) const {
+        const float t = g * lr;
+        return w - t;
+    }
+};
 
 // ------------------------------------------------------ affine forward
-
-// y = act(x*scale[j] + bias[j]) over [m, n], n % 4 == 0.  A thread owns one
-// float4 of columns (scale and bias loaded once) and UNR rows at a time.
-template <int ACT, int UNR>
-__global__ __launch_bounds__(kBlock) void k_affine_fwd_vec(const float *__restrict__ x,
-                                                           const float *__restrict__ scale,
-                                                           const float *__restrict__ bias,
-                                                           float *__restrict__ y, size_t m, size_t n,
-                                                           size_t rows_per_chunk) {
-    const size_t j4 = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (4 * j4 >= n) return;
-    const float4 s = ld4(scale + 4 * j4);
-    const float4 b = ld4(bias + 4 * j4);
-    const size_t r0 = static_cast<size_t>(blockIdx.y) * rows_per_chunk;
-    const size_t r1 = r0 + rows_per_chunk < m ? r0 + rows_per_chunk : m;
-    size_t r = r0;
-    for (; r + UNR <= r1; r += UNR) {
-        float4 v[UNR];
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) v[u] = ld4_stream(x + (r + u) * n + 4 * j4);
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            float4 t;
-            t.x = v[u].x * s.x; t.y = v[u].y * s.y; t.z = v[u].z * s.z; t.w = v[u].w * s.w;
-            t.x = t.x + b.x; t.y = t.y + b.y; t.z = t.z + b.z; t.w = t.w + b.w;
-            st4_stream(y + (r + u) * n + 4 * j4, act4<ACT>(t));
-        }
-    }
-    for (; r < r1; ++r) {
-        const float4 v = ld4_stream(x + r * n + 4 * j4);
-        float4 t;
-        t.x = v.x * s.x; t.y = v.y * s.y; t.z = v.z * s.z; t.w = v.w * s.w;
-        t.x = t.x + b.x; t.y = t.y + b.y; t.z = t.z + b.z; t.w = t.w + b.w;
-        st4_stream(y + r * n + 4 * j4, act4<ACT>(t));
-    }
-}
 
 template <int ACT>
 __global__ __launch_bounds__(kBlock) void k_affine_fwd_scalar(const float *x, const float *scale,
@@ -398,30 +344,11 @@ __global__ __launch_bounds__(NW * kWave) void k_affine_bwd(const float *__restri
 // ------------------------------------------------------------------ sgd
 
 // w = w - g*lr, two roundings (matrix_t::sub of ScalarOp::mul).
-__global__ __launch_bounds__(kBlock) void k_sgd(float *w, const float *__restrict__ g, float lr,
-                                                size_t n, int vec) {
+__global__ __launch_bounds__(kBlock) void k_sgd_scalar(float *w, const float *g, float lr, size_t n) {
     const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-    size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (vec) {
-        const size_t n4 = n / 4;
-        for (; i < n4; i += stride) {
-            const float4 gv = ld4(g + 4 * i);
-            float4 wv = ld4(w + 4 * i);
-            float4 t;
-            t.x = gv.x * lr; t.y = gv.y * lr; t.z = gv.z * lr; t.w = gv.w * lr;
-            wv.x = wv.x - t.x; wv.y = wv.y - t.y; wv.z = wv.z - t.z; wv.w = wv.w - t.w;
-            st4(w + 4 * i, wv);
-        }
-        if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
-            const size_t j = 4 * n4 + threadIdx.x;
-            const float t = g[j] * lr;
-            w[j] = w[j] - t;
-        }
-    } else {
-        for (; i < n; i += stride) {
-            const float t = g[i] * lr;
-            w[i] = w[i] - t;
-        }
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        const float t = g[i] * lr;
+        w[i] = w[i] - t;
     }
 }
 
@@ -446,7 +373,9 @@ int dispatch_op(int op, A... a) {
 template <int OP>
 struct BinaryL {
     static int run(const float *x, const float *y, float *z, size_t n, hipStream_t s) {
-        hipLaunchKernelGGL(k_binary_vec<OP>, dim3(stream_grid(n / 4)), dim3(kBlock), 0, s, x, y, z, n);
+        const unsigned g = map4_grid(n);
+        if (!g) return CXM_E_TOO_LARGE;
+        hipLaunchKernelGGL(k_zip4<BinF<OP>>, dim3(g), dim3(kBlock), 0, s, BinF<OP>{}, x, y, z, n);
         return launch_status();
     }
 };
@@ -454,34 +383,25 @@ struct BinaryL {
 template <int OP>
 struct ScalarL {
     static int run(const float *x, float v, float *z, size_t n, hipStream_t s) {
-        hipLaunchKernelGGL(k_scalar_vec<OP>, dim3(stream_grid(n / 4)), dim3(kBlock), 0, s, x, v, z, n);
+        const unsigned g = map4_grid(n);
+        if (!g) return CXM_E_TOO_LARGE;
+        hipLaunchKernelGGL(k_map4<ScalarF<OP>>, dim3(g), dim3(kBlock), 0, s, ScalarF<OP>{v}, x, z, n);
         return launch_status();
     }
 };
-
-// grid for the [m, n] column-tile x row-chunk kernels
-inline void tile_grid(size_t m, size_t n, dim3 *grid, size_t *rpc) {
-    const size_t tiles = (n / 4 + kBlock - 1) / kBlock;
-    size_t chunks = (4096 + tiles - 1) / tiles;
-    if (chunks > m) chunks = m;
-    if (chunks < 1) chunks = 1;
-    if (chunks > 65535) chunks = 65535;
-    *rpc = (m + chunks - 1) / chunks;
-    chunks = (m + *rpc - 1) / *rpc;
-    *grid = dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(chunks));
-}
 
 template <int OP>
 struct BcastL {
     static int run(const float *x, const float *y, float *z, size_t m, size_t n, int row_mode,
                    hipStream_t s) {
-        dim3 grid;
-        size_t rpc;
-        tile_grid(m, n, &grid, &rpc);
+        unsigned grid, tpr;
+        if (!rowmap4_grid(m, n / 4, &grid, &tpr)) return CXM_E_TOO_LARGE;
         if (row_mode)
-            hipLaunchKernelGGL(k_bcast_row_vec<OP>, grid, dim3(kBlock), 0, s, x, y, z, m, n, rpc);
+            hipLaunchKernelGGL(k_rowmap4<RowBcastF<OP>>, dim3(grid), dim3(kBlock), 0, s, RowBcastF<OP>{y}, x, z,
+                               n / 4, tpr);
         else
-            hipLaunchKernelGGL(k_bcast_col_vec<OP>, grid, dim3(kBlock), 0, s, x, y, z, m, n, rpc);
+            hipLaunchKernelGGL(k_rowmap4<ColBcastF<OP>>, dim3(grid), dim3(kBlock), 0, s, ColBcastF<OP>{y}, x, z,
+                               n / 4, tpr);
         return launch_status();
     }
 };
@@ -499,23 +419,24 @@ int bcast(const float *x, const float *y, float *z, size_t m, size_t n, int op, 
 
 template <int ACT>
 int unary_t(const float *x, float *z, size_t n, hipStream_t s) {
-    if (aligned16(x) && aligned16(z))
-        hipLaunchKernelGGL((k_unary<ACT, true>), dim3(stream_grid(n / 4)), dim3(kBlock), 0, s, x, z, n);
-    else
-        hipLaunchKernelGGL((k_unary<ACT, false>), dim3(stream_grid((n + 3) / 4)), dim3(kBlock), 0, s, x,
-                           z, n);
+    if (aligned16(x) && aligned16(z)) {
+        const unsigned g = map4_grid(n);
+        if (!g) return CXM_E_TOO_LARGE;
+        hipLaunchKernelGGL(k_map4<ActF<ACT>>, dim3(g), dim3(kBlock), 0, s, ActF<ACT>{}, x, z, n);
+    } else {
+        hipLaunchKernelGGL(k_unary_scalar<ACT>, dim3(stream_grid((n + 3) / 4)), dim3(kBlock), 0, s, x, z, n);
+    }
     return launch_status();
 }
 
 template <int ACT>
 int affine_fwd_t(const float *x, const float *scale, const float *bias, float *y, size_t m,
                  size_t n, hipStream_t s) {
-    if (n % 4 == 0 && aligned16(x) && aligned16(scale) && aligned16(bias) && aligned16(y)) {
-        dim3 grid;
-        size_t rpc;
-        tile_grid(m, n, &grid, &rpc);
-        hipLaunchKernelGGL((k_affine_fwd_vec<ACT, 4>), grid, dim3(kBlock), 0, s, x, scale, bias, y, m,
-                           n, rpc);
+    unsigned grid, tpr;
+    if (n % 4 == 0 && aligned16(x) && aligned16(scale) && aligned16(bias) && aligned16(y) &&
+        rowmap4_grid(m, n / 4, &grid, &tpr)) {
+        hipLaunchKernelGGL(k_rowmap4<AffineF<ACT>>, dim3(grid), dim3(kBlock), 0, s, AffineF<ACT>{scale, bias},
+                           x, y, n / 4, tpr);
     } else {
         hipLaunchKernelGGL(k_affine_fwd_scalar<ACT>, dim3(stream_grid((m * n + 3) / 4)), dim3(kBlock), 0,
                            s, x, scale, bias, y, m, n);
@@ -524,10 +445,13 @@ int affine_fwd_t(const float *x, const float *scale, const float *bias, float *y
 }
 
 // Row chunks per column tile and launch order.  Measured on gfx950 at 256 MiB
-// per operand: 512 workgroups of 4 waves (two per CU, each streaming a few
-// hundred rows) reach 6.1-6.2 TB/s at [8192, 8192] and [1024, 65536], where
-// 2048 shorter workgroups stay near 5.4 TB/s and 384 leave CUs unevenly
-// loaded; 16-wave workgroups were slower at every square or wide shape.
+// per operand, sigmoid: 512 workgroups of 4 waves (two per CU, each
+// streaming a few hundred rows), one row of loads per wave in flight and
+// the chunks of a tile adjacent in launch order reach 6.5 TB/s at
+// [8192, 8192] and 6.7 TB/s at [1024, 65536].  Deeper unrolling (2 or 4
+// rows of loads per wave, with or without a scheduling barrier that keeps
+// them together), 2048 shorter workgroups, 384 workgroups (CUs unevenly
+// loaded) and 16-wave workgroups were all slower, by 5-25%.
 struct AffBwdPlan {
     size_t chunks;   // 0: enough for about 512 workgroups
     int tile_major;  // chunks of one tile adjacent in launch order
@@ -560,11 +484,11 @@ int affine_bwd_plan(const float *x, const float *scale, const float *y, const fl
     }
     const dim3 grid(static_cast<unsigned>(ntiles * chunks));
     const unsigned nt = static_cast<unsigned>(ntiles), nc = static_cast<unsigned>(chunks);
-#define CXM_AFFB(VEC_, UNR_, NW_)                                                                       \
-    hipLaunchKernelGGL((k_affine_bwd<ACT, VEC_, UNR_, NW_>), grid, dim3(NW_ * kWave), 0, hs(st), x, scale, y, dy, \
-                       dx, dscale, dbias, m, n, nt, nc, rpc, plan.tile_major, part, counters)
-    if (vec) CXM_AFFB(true, 4, 4);
-    else CXM_AFFB(false, 1, 4);
+#define CXM_AFFB(VEC_)                                                                                  \
+    hipLaunchKernelGGL((k_affine_bwd<ACT, VEC_, 1, 4>), grid, dim3(4 * kWave), 0, hs(st), x, scale, y, dy, dx,    \
+                       dscale, dbias, m, n, nt, nc, rpc, plan.tile_major, part, counters)
+    if (vec) CXM_AFFB(true);
+    else CXM_AFFB(false);
 #undef CXM_AFFB
     return launch_status();
 }
@@ -657,9 +581,13 @@ int cxm_affine_act_bwd_f32(const float *x, const float *scale, const float *y, c
 int cxm_sgd_f32(float *w, const float *g, float lr, size_t n, cxm_stream_t s) {
     if (!w || !g) return CXM_E_INVALID;
     if (n == 0) return CXM_OK;
-    const int vec = aligned16(w) && aligned16(g);
-    hipLaunchKernelGGL(k_sgd, dim3(stream_grid(vec ? n / 4 : (n + 3) / 4)), dim3(kBlock), 0, hs(s), w, g,
-                       lr, n, vec);
+    if (aligned16(w) && aligned16(g)) {
+        const unsigned grid = map4_grid(n);
+        if (!grid) return CXM_E_TOO_LARGE;
+        hipLaunchKernelGGL(k_zip4<SgdF>, dim3(grid), dim3(kBlock), 0, hs(s), SgdF{lr}, w, g, w, n);
+    } else {
+        hipLaunchKernelGGL(k_sgd_scalar, dim3(stream_grid((n + 3) / 4)), dim3(kBlock), 0, hs(s), w, g, lr, n);
+    }
     return launch_status();
 }
 

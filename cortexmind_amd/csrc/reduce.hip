@@ -1,8 +1,9 @@
-// fp32 reductions sum / mean / max / argmax, flat and over the middle axis
+// fp32 reductions sum / mean / max / argmax / min / argmin / norm1 / norm2 /
+// var / stdv, flat and over the middle axis
 // of [outer, dim, inner].
 //
 // Replaces avx2::reduce (source/CortexMind/framework/Engine/AVX2/
-// reduce.hpp:49-296, reduce.cpp:17-84, 204-251, 439-528).  Semantics the
+// reduce.hpp:49-329, reduce.cpp:17-621).  Semantics the
 // kernels keep from it are listed in include/cxm_hip.h.
 //
 // Two kernels cover every shape:
@@ -23,13 +24,20 @@
 namespace cxm {
 namespace {
 
-// Max over a column path starts from the first slice (reduce.cpp:230-236),
-// which is the same as starting from -inf.
+// Max / min over a column path start from the first slice (reduce.cpp:
+// 230-236, 285-293), which is the same as starting from -inf / +inf.
 struct MaxColOp : MaxOp {
     __device__ static T identity() { return -INFINITY; }
 };
+struct MinColOp : MinOp {
+    __device__ static T identity() { return INFINITY; }
+};
 
-enum OutKind : int { kOutValue = 0, kOutMean = 1, kOutIndex = 2, kOutSgd = 3 };
+// kOutMean / kOutVar scale like reduce.cpp:77-83 / 173-182: outputs below
+// `body` multiply by inv (= 1/dim), the rest divide by dimf.
+enum OutKind : int {
+    kOutValue = 0, kOutMean = 1, kOutIndex = 2, kOutSgd = 3, kOutSqrt = 4, kOutVar = 5, kOutStd = 6
+};
 
 struct OutDesc {
     void *z;
@@ -41,8 +49,17 @@ struct OutDesc {
 
 template <class Op>
 __device__ __forceinline__ void write_out(const OutDesc &o, size_t q, typename Op::T r) {
-    if constexpr (std::is_same_v<Op, ArgMaxOp>) {
+    if constexpr (std::is_same_v<typename Op::T, ArgPair>) {
         static_cast<int32_t *>(o.z)[q] = r.i;
+    } else if constexpr (std::is_same_v<typename Op::T, Pow2>) {
+        // sum of squared deviations, rounded once to fp32, then scaled as
+        // reduce.cpp scales it (population variance)
+        const double n = o.dimf;
+        const double m2d = r.s2 - r.s1 * (r.s1 / n);
+        const float m2 = m2d > 0.0 ? static_cast<float>(m2d) : 0.0f;
+        float v = q < o.body ? m2 * o.inv : m2 / o.dimf;
+        if (o.kind == kOutStd) v = __builtin_sqrtf(v);
+        static_cast<float *>(o.z)[q] = v;
     } else {
         float v = r;
         float *z = static_cast<float *>(o.z);
@@ -52,16 +69,27 @@ __device__ __forceinline__ void write_out(const OutDesc &o, size_t q, typename O
             return;
         }
         if (o.kind == kOutMean) v = q < o.body ? v * o.inv : v / o.dimf;
+        if (o.kind == kOutSqrt) v = __builtin_sqrtf(v);
         z[q] = v;
     }
 }
 
+// Component c of v has index base + c*cstep (rows: consecutive elements,
+// cstep 1; columns: four columns of one row, cstep 0).  kShift operators
+// get v - k (k: the first element of each component's row or column).
 template <class Op>
-__device__ __forceinline__ void fold4(typename Op::T (&acc)[4], const float4 v, int base) {
-    acc[0] = Op::combine(acc[0], Op::from(v.x, base + 0));
-    acc[1] = Op::combine(acc[1], Op::from(v.y, base + 1));
-    acc[2] = Op::combine(acc[2], Op::from(v.z, base + 2));
-    acc[3] = Op::combine(acc[3], Op::from(v.w, base + 3));
+__device__ __forceinline__ void fold4(typename Op::T (&acc)[4], float4 v, int base, int cstep,
+                                      float4 k) {
+    if constexpr (Op::kShift) {
+        v.x = v.x - k.x;
+        v.y = v.y - k.y;
+        v.z = v.z - k.z;
+        v.w = v.w - k.w;
+    }
+    acc[0] = Op::accum(acc[0], v.x, base);
+    acc[1] = Op::accum(acc[1], v.y, base + cstep);
+    acc[2] = Op::accum(acc[2], v.z, base + 2 * cstep);
+    acc[3] = Op::accum(acc[3], v.w, base + 3 * cstep);
 }
 
 // ------------------------------------------------------------------ rows
@@ -86,6 +114,9 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
     const int tid = threadIdx.x;
 
     T acc[4] = {Op::identity(), Op::identity(), Op::identity(), Op::identity()};
+    float k = 0.0f;
+    if constexpr (Op::kShift) k = xr[0];
+    const float4 k4 = make_float4(k, k, k, k);
     if constexpr (VEC) {
         const size_t e4 = end / 4;
         size_t i = begin / 4 + tid;
@@ -94,12 +125,15 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
 #pragma unroll
             for (int u = 0; u < UNR; ++u) v[u] = ld4_stream(xr + 4 * (i + u * kBlock));
 #pragma unroll
-            for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], static_cast<int>(4 * (i + u * kBlock)));
+            for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], static_cast<int>(4 * (i + u * kBlock)), 1, k4);
         }
-        for (; i < e4; i += kBlock) fold4<Op>(acc, ld4_stream(xr + 4 * i), static_cast<int>(4 * i));
+        for (; i < e4; i += kBlock) fold4<Op>(acc, ld4_stream(xr + 4 * i), static_cast<int>(4 * i), 1, k4);
     } else {
-        for (size_t i = begin + tid; i < end; i += kBlock)
-            acc[0] = Op::combine(acc[0], Op::from(xr[i], static_cast<int>(i)));
+        for (size_t i = begin + tid; i < end; i += kBlock) {
+            float v = xr[i];
+            if constexpr (Op::kShift) v = v - k;
+            acc[0] = Op::accum(acc[0], v, static_cast<int>(i));
+        }
     }
     T r = Op::combine(Op::combine(acc[0], acc[1]), Op::combine(acc[2], acc[3]));
     r = block_reduce<Op, kBlock>(r, lds);
@@ -165,28 +199,17 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
         T acc[4] = {Op::identity(), Op::identity(), Op::identity(), Op::identity()};
         if (col < inner) {
             const float *__restrict__ xc = xo + col;
+            float4 k4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if constexpr (Op::kShift) k4 = ld4(xc);
             size_t r = r0 + w;
             for (; r + (UNR - 1) * NW < r1; r += UNR * NW) {
                 float4 v[UNR];
 #pragma unroll
                 for (int u = 0; u < UNR; ++u) v[u] = ld4_stream(xc + (r + u * NW) * inner);
 #pragma unroll
-                for (int u = 0; u < UNR; ++u) {
-                    const int ri = static_cast<int>(r + u * NW);
-                    acc[0] = Op::combine(acc[0], Op::from(v[u].x, ri));
-                    acc[1] = Op::combine(acc[1], Op::from(v[u].y, ri));
-                    acc[2] = Op::combine(acc[2], Op::from(v[u].z, ri));
-                    acc[3] = Op::combine(acc[3], Op::from(v[u].w, ri));
-                }
+                for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], static_cast<int>(r + u * NW), 0, k4);
             }
-            for (; r < r1; r += NW) {
-                const float4 v = ld4_stream(xc + r * inner);
-                const int ri = static_cast<int>(r);
-                acc[0] = Op::combine(acc[0], Op::from(v.x, ri));
-                acc[1] = Op::combine(acc[1], Op::from(v.y, ri));
-                acc[2] = Op::combine(acc[2], Op::from(v.z, ri));
-                acc[3] = Op::combine(acc[3], Op::from(v.w, ri));
-            }
+            for (; r < r1; r += NW) fold4<Op>(acc, ld4_stream(xc + r * inner), static_cast<int>(r), 0, k4);
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) lds[w][lane * 4 + c] = acc[c];
@@ -194,9 +217,15 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
         const int c = tid % kColTile, ph = tid / kColTile;
         const size_t col = static_cast<size_t>(tile) * kColTile + c;
         T mine = Op::identity();
-        if (col < inner)
-            for (size_t r = r0 + ph; r < r1; r += NSLOT)
-                mine = Op::combine(mine, Op::from(xo[r * inner + col], static_cast<int>(r)));
+        if (col < inner) {
+            float k = 0.0f;
+            if constexpr (Op::kShift) k = xo[col];
+            for (size_t r = r0 + ph; r < r1; r += NSLOT) {
+                float v = xo[r * inner + col];
+                if constexpr (Op::kShift) v = v - k;
+                mine = Op::accum(mine, v, static_cast<int>(r));
+            }
+        }
         lds[ph][c] = mine;
     }
     __syncthreads();
@@ -338,30 +367,53 @@ int run_cols(const float *x, size_t outer, size_t dim, size_t inner, OutDesc out
     return run_cols_plan<Op>(x, outer, dim, inner, out, col_plan(tiles, dim), s);
 }
 
-enum Which { kSum, kMean, kMax, kArgMax };
+enum Which { kSum, kMean, kMax, kArgMax, kMin, kArgMin, kNorm1, kNorm2, kVar, kStdv };
+
+OutKind out_kind(Which w) {
+    switch (w) {
+        case kMean: return kOutMean;
+        case kArgMax:
+        case kArgMin: return kOutIndex;
+        case kNorm2: return kOutSqrt;
+        case kVar: return kOutVar;
+        case kStdv: return kOutStd;
+        default: return kOutValue;
+    }
+}
 
 int reduce_axis(Which which, const float *x, void *z, size_t outer, size_t dim, size_t inner,
                 cxm_stream_t s) {
     if (!x || !z) return CXM_E_INVALID;
     if (outer == 0 || inner == 0) return CXM_OK;  // empty output
     if (dim == 0) return CXM_E_INVALID;
-    if (which == kArgMax && dim > 0x7fffffffu) return CXM_E_TOO_LARGE;
+    if ((which == kArgMax || which == kArgMin) && dim > 0x7fffffffu) return CXM_E_TOO_LARGE;
     const size_t total = outer * inner;
-    OutDesc out{z, which == kMean ? kOutMean : (which == kArgMax ? kOutIndex : kOutValue),
-                total - total % 8, 1.0f / static_cast<float>(dim), static_cast<float>(dim)};
+    // var over rows divides (reduce.cpp:135); over columns it scales like mean
+    const size_t body = (which == kVar || which == kStdv) && inner == 1 ? 0 : total - total % 8;
+    OutDesc out{z, out_kind(which), body, 1.0f / static_cast<float>(dim), static_cast<float>(dim)};
     if (inner == 1) {
         switch (which) {
             case kSum:
             case kMean: return run_rows<SumOp>(x, outer, dim, out, s);
             case kMax: return run_rows<MaxOp>(x, outer, dim, out, s);
-            default: return run_rows<ArgMaxOp>(x, outer, dim, out, s);
+            case kArgMax: return run_rows<ArgMaxOp>(x, outer, dim, out, s);
+            case kMin: return run_rows<MinOp>(x, outer, dim, out, s);
+            case kArgMin: return run_rows<ArgMinOp>(x, outer, dim, out, s);
+            case kNorm1: return run_rows<AbsSumOp>(x, outer, dim, out, s);
+            case kNorm2: return run_rows<SqSumOp>(x, outer, dim, out, s);
+            default: return run_rows<Pow2Op>(x, outer, dim, out, s);
         }
     }
     switch (which) {
         case kSum:
         case kMean: return run_cols<SumOp>(x, outer, dim, inner, out, s);
         case kMax: return run_cols<MaxColOp>(x, outer, dim, inner, out, s);
-        default: return run_cols<ArgMaxOp>(x, outer, dim, inner, out, s);
+        case kArgMax: return run_cols<ArgMaxOp>(x, outer, dim, inner, out, s);
+        case kMin: return run_cols<MinColOp>(x, outer, dim, inner, out, s);
+        case kArgMin: return run_cols<ArgMinOp>(x, outer, dim, inner, out, s);
+        case kNorm1: return run_cols<AbsSumOp>(x, outer, dim, inner, out, s);
+        case kNorm2: return run_cols<SqSumOp>(x, outer, dim, inner, out, s);
+        default: return run_cols<Pow2Op>(x, outer, dim, inner, out, s);
     }
 }
 
@@ -369,21 +421,30 @@ int reduce_flat(Which which, const float *x, void *z, size_t n, cxm_stream_t s) 
     if (!z) return CXM_E_INVALID;
     hipStream_t hs = reinterpret_cast<hipStream_t>(s);
     if (n == 0) {
-        // reduce.cpp:17-28 / 66-69 / 204-215 on zero elements: 0, 0/0, -FLT_MAX.
-        if (which == kArgMax) return CXM_E_INVALID;  // the reference reads x[0]
-        const float v = which == kSum ? 0.0f : (which == kMean ? NAN : -FLT_MAX);
+        // The reference on zero elements: sum/norm1/norm2 0 (reduce.cpp:17-28,
+        // 311-322, 369-381), mean/var/stdv 0/0 (:66-69, 86-104), max -FLT_MAX
+        // (:204-215), min FLT_MAX (:253-264).  argmax/argmin read x[0].
+        if (which == kArgMax || which == kArgMin) return CXM_E_INVALID;
+        float v = 0.0f;
+        if (which == kMean || which == kVar || which == kStdv) v = NAN;
+        if (which == kMax) v = -FLT_MAX;
+        if (which == kMin) v = FLT_MAX;
         hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(1), 0, hs, static_cast<float *>(z), v);
         return launch_status();
     }
     if (!x) return CXM_E_INVALID;
-    if (which == kArgMax && n > 0x7fffffffu) return CXM_E_TOO_LARGE;
-    OutDesc out{z, which == kMean ? kOutMean : (which == kArgMax ? kOutIndex : kOutValue), 0,
-                0.0f, static_cast<float>(n)};
+    if ((which == kArgMax || which == kArgMin) && n > 0x7fffffffu) return CXM_E_TOO_LARGE;
+    OutDesc out{z, out_kind(which), 0, 0.0f, static_cast<float>(n)};
     switch (which) {
         case kSum:
         case kMean: return run_rows<SumOp>(x, 1, n, out, s);
         case kMax: return run_rows<MaxOp>(x, 1, n, out, s);
-        default: return run_rows<ArgMaxOp>(x, 1, n, out, s);
+        case kArgMax: return run_rows<ArgMaxOp>(x, 1, n, out, s);
+        case kMin: return run_rows<MinOp>(x, 1, n, out, s);
+        case kArgMin: return run_rows<ArgMinOp>(x, 1, n, out, s);
+        case kNorm1: return run_rows<AbsSumOp>(x, 1, n, out, s);
+        case kNorm2: return run_rows<SqSumOp>(x, 1, n, out, s);
+        default: return run_rows<Pow2Op>(x, 1, n, out, s);
     }
 }
 
@@ -428,5 +489,21 @@ int cxm_reduce_argmax_f32(const float *x, int32_t *z, size_t outer, size_t dim, 
                           cxm_stream_t s) {
     return cxm::reduce_axis(cxm::kArgMax, x, z, outer, dim, inner, s);
 }
+
+#define CXM_REDUCE_ENTRY(NAME, WHICH, ZT)                                                            \
+    int cxm_reduce_##NAME##_flat_f32(const float *x, ZT *z, size_t n, cxm_stream_t s) {             \
+        return cxm::reduce_flat(cxm::WHICH, x, z, n, s);                                           \
+    }                                                                                               \
+    int cxm_reduce_##NAME##_f32(const float *x, ZT *z, size_t outer, size_t dim, size_t inner,     \
+                                cxm_stream_t s) {                                                   \
+        return cxm::reduce_axis(cxm::WHICH, x, z, outer, dim, inner, s);                           \
+    }
+CXM_REDUCE_ENTRY(min, kMin, float)
+CXM_REDUCE_ENTRY(argmin, kArgMin, int32_t)
+CXM_REDUCE_ENTRY(norm1, kNorm1, float)
+CXM_REDUCE_ENTRY(norm2, kNorm2, float)
+CXM_REDUCE_ENTRY(var, kVar, float)
+CXM_REDUCE_ENTRY(stdv, kStdv, float)
+#undef CXM_REDUCE_ENTRY
 
 }  // extern "C"

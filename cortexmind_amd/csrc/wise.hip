@@ -59,39 +59,14 @@ struct FClamp {
 };
 
 template <class F>
-__device__ __forceinline__ float4 map4(const F &f, float4 v) {
-    return make_float4(f(v.x), f(v.y), f(v.z), f(v.w));
-}
-
-// 16-byte aligned x and z: float4 grid-stride body, two float4 per thread
-// per iteration, tail (n % 4) by the first threads of workgroup 0.  z may
-// alias x: every element is read and written by the same thread.
-template <class F>
-__global__ __launch_bounds__(kBlock) void k_map_vec(F f, const float *x, float *z, size_t n) {
-    const size_t n4 = n / 4;
-    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-    size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    for (; i + stride < n4; i += 2 * stride) {
-        const float4 a = ld4(x + 4 * i), b = ld4(x + 4 * (i + stride));
-        st4(z + 4 * i, map4(f, a));
-        st4(z + 4 * (i + stride), map4(f, b));
-    }
-    if (i < n4) st4(z + 4 * i, map4(f, ld4(x + 4 * i)));
-    if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
-        const size_t j = 4 * n4 + threadIdx.x;
-        z[j] = f(x[j]);
-    }
-}
-
-template <class F>
 __global__ __launch_bounds__(kBlock) void k_map_any(F f, const float *x, float *z, size_t n) {
     const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
     for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
         z[i] = f(x[i]);
 }
 
-// Same launch shape as the other streaming kernels: at most 16 workgroups
-// per CU, each thread striding through the rest.
+// Grid-stride launch for the unaligned and gather kernels: at most 16
+// workgroups per CU, each thread striding through the rest.
 inline unsigned map_grid(size_t units) {
     size_t b = (units + kBlock - 1) / kBlock;
     const size_t cap = 256 * 16;
@@ -100,12 +75,17 @@ inline unsigned map_grid(size_t units) {
 
 inline hipStream_t hs(cxm_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// 16-byte aligned: the one-float4-per-thread streaming map; otherwise a
+// scalar grid-stride loop.
 template <class F>
 int map(F f, const float *x, float *z, size_t n, cxm_stream_t s) {
-    if (aligned16(x) && aligned16(z))
-        hipLaunchKernelGGL(k_map_vec<F>, dim3(map_grid((n / 4 + 1) / 2)), dim3(kBlock), 0, hs(s), f, x, z, n);
-    else
+    if (aligned16(x) && aligned16(z)) {
+        const unsigned g = map4_grid(n);
+        if (!g) return CXM_E_TOO_LARGE;
+        hipLaunchKernelGGL(k_map4<F>, dim3(g), dim3(kBlock), 0, hs(s), f, x, z, n);
+    } else {
         hipLaunchKernelGGL(k_map_any<F>, dim3(map_grid(n)), dim3(kBlock), 0, hs(s), f, x, z, n);
+    }
     return launch_status();
 }
 

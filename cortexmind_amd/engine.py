@@ -58,6 +58,30 @@ class reduce:
     def argmax(Xx, Xz, *sizes, stream=None):
         reduce._run("argmax", Xx, Xz, sizes, stream)
 
+    @staticmethod
+    def min(Xx, Xz, *sizes, stream=None):
+        reduce._run("min", Xx, Xz, sizes, stream)
+
+    @staticmethod
+    def argmin(Xx, Xz, *sizes, stream=None):
+        reduce._run("argmin", Xx, Xz, sizes, stream)
+
+    @staticmethod
+    def norm1(Xx, Xz, *sizes, stream=None):
+        reduce._run("norm1", Xx, Xz, sizes, stream)
+
+    @staticmethod
+    def norm2(Xx, Xz, *sizes, stream=None):
+        reduce._run("norm2", Xx, Xz, sizes, stream)
+
+    @staticmethod
+    def var(Xx, Xz, *sizes, stream=None):
+        reduce._run("var", Xx, Xz, sizes, stream)
+
+    @staticmethod
+    def stdv(Xx, Xz, *sizes, stream=None):
+        reduce._run("stdv", Xx, Xz, sizes, stream)
+
 
 class _BcastAxis:
     def __init__(self, fn):

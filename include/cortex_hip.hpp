@@ -63,6 +63,27 @@ struct reduce {
                        std::size_t inner) {
         check(cxm_reduce_argmax_f32(Xx, Xz, outer, dim, inner, stream()), "reduce::argmax");
     }
+    static void argmin(const float *Xx, std::int32_t *Xz, std::size_t N) {
+        check(cxm_reduce_argmin_flat_f32(Xx, Xz, N, stream()), "reduce::argmin");
+    }
+    static void argmin(const float *Xx, std::int32_t *Xz, std::size_t outer, std::size_t dim,
+                       std::size_t inner) {
+        check(cxm_reduce_argmin_f32(Xx, Xz, outer, dim, inner, stream()), "reduce::argmin");
+    }
+#define CXM_HIP_REDUCE(NAME)                                                                        \
+    static void NAME(const float *Xx, float *Xz, std::size_t N) {                                   \
+        check(cxm_reduce_##NAME##_flat_f32(Xx, Xz, N, stream()), "reduce::" #NAME);                 \
+    }                                                                                               \
+    static void NAME(const float *Xx, float *Xz, std::size_t outer, std::size_t dim, std::size_t inner) { \
+        check(cxm_reduce_##NAME##_f32(Xx, Xz, outer, dim, inner, stream()), "reduce::" #NAME);      \
+    }
+    // reduce.hpp:96-263: var, stdv, min, norm1, norm2
+    CXM_HIP_REDUCE(var)
+    CXM_HIP_REDUCE(stdv)
+    CXM_HIP_REDUCE(min)
+    CXM_HIP_REDUCE(norm1)
+    CXM_HIP_REDUCE(norm2)
+#undef CXM_HIP_REDUCE
 };
 
 // avx2::Broadcast::row / ::col (broadcast.hpp:20-57): out-of-place

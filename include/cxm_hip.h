@@ -126,6 +126,43 @@ int cxm_reduce_max_f32(const float *x, float *z, size_t outer, size_t dim, size_
                        cxm_stream_t s);
 int cxm_reduce_argmax_f32(const float *x, int32_t *z, size_t outer, size_t dim, size_t inner,
                           cxm_stream_t s);
+/* The rest of avx2::reduce (Engine/AVX2/reduce.hpp:96-329), same two forms:
+ *  - min (reduce.cpp:253-309): smallest value; the flat and row forms start
+ *    from FLT_MAX (an all-+inf input gives FLT_MAX), the column form from
+ *    the first slice.  Exact.
+ *  - argmin (reduce.cpp:530-621): int32 index of the first minimum.  Exact.
+ *  - norm1 (reduce.cpp:311-367): sum of |x|.
+ *  - norm2 (reduce.cpp:369-437): sqrt of the sum of x*x (products unrounded,
+ *    as fma::add).
+ *  - var (reduce.cpp:86-183): population variance, sum((x - mean)^2) / dim;
+ *    flat and row results divide by the count, column results multiply by
+ *    1/dim except the last total % 8 outputs, which divide (reduce.cpp:
+ *    173-182).  One pass over x, where the reference reads it twice: the
+ *    device sums d and d*d in fp64 with d = x - (first element of the row
+ *    or column), so there is no cancellation between large sums.
+ *  - stdv (reduce.cpp:185-202): sqrt(var).
+ * Sums, norms and variances are within 1e-5 relative of the exact value for
+ * the data sizes of the reference workloads.  n == 0 gives what the
+ * reference's loops give (min FLT_MAX, norms 0, var/stdv NaN); argmin of
+ * zero elements is CXM_E_INVALID. */
+int cxm_reduce_min_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s);
+int cxm_reduce_argmin_flat_f32(const float *x, int32_t *z, size_t n, cxm_stream_t s);
+int cxm_reduce_norm1_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s);
+int cxm_reduce_norm2_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s);
+int cxm_reduce_var_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s);
+int cxm_reduce_stdv_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s);
+int cxm_reduce_min_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                       cxm_stream_t s);
+int cxm_reduce_argmin_f32(const float *x, int32_t *z, size_t outer, size_t dim, size_t inner,
+                          cxm_stream_t s);
+int cxm_reduce_norm1_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                         cxm_stream_t s);
+int cxm_reduce_norm2_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                         cxm_stream_t s);
+int cxm_reduce_var_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                       cxm_stream_t s);
+int cxm_reduce_stdv_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                        cxm_stream_t s);
 
 /* ------------------------------------------------------------ elementwise
  * Same-shape binary z = x op y: matrix_t::{add,sub,mul,div,max,min}

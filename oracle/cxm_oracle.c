@@ -59,6 +59,27 @@ static float fold_max8(const float a[L8]) {
     return simd_max(n0, n1);
 }
 
+/* _mm_min_ps / _mm256_min_ps(a, b): returns a when a < b, else b. */
+static inline float simd_min(float a, float b) { return a < b ? a : b; }
+/* std::min(a, b): returns b when b < a, else a. */
+static inline float std_min(float a, float b) { return b < a ? b : a; }
+
+/* horizontal::min (horizontal.hpp:95-102): min(lo,hi), movehl, shuffle 1. */
+static float fold_min8(const float a[L8]) {
+    const float m0 = simd_min(a[0], a[4]), m1 = simd_min(a[1], a[5]);
+    const float m2 = simd_min(a[2], a[6]), m3 = simd_min(a[3], a[7]);
+    const float n0 = simd_min(m0, m2), n1 = simd_min(m1, m3);
+    return simd_min(n0, n1);
+}
+
+/* horizontal::argmin (horizontal.hpp:171-176): first lane equal to the min. */
+static int fold_argmin8(const float a[L8]) {
+    const float m = fold_min8(a);
+    for (int l = 0; l < L8; ++l)
+        if (a[l] == m) return l;
+    return -1;
+}
+
 /* horizontal::argmax (horizontal.hpp:154-159): first lane equal to the max. */
 static int fold_argmax8(const float a[L8]) {
     const float m = fold_max8(a);
@@ -205,6 +226,266 @@ void orc_reduce_argmax(const float *x, int32_t *z, size_t outer, size_t dim, siz
         }
     }
     free(best);
+}
+
+/* ------------------------------------------------------------------ min */
+
+/* reduce::min flat (reduce.cpp:253-264): lanes start at FLT_MAX. */
+void orc_reduce_min_flat(const float *x, float *z, size_t n) {
+    float acc[L8];
+    for (int l = 0; l < L8; ++l) acc[l] = FLT_MAX;
+    size_t i = 0;
+    for (; i + L8 <= n; i += L8)
+        for (int l = 0; l < L8; ++l) acc[l] = simd_min(acc[l], x[i + l]);
+    float r = fold_min8(acc);
+    for (; i < n; ++i) r = std_min(r, x[i]);
+    z[0] = r;
+}
+
+/* reduce::min axis (reduce.cpp:266-309): inner==1 -> the flat loop per row;
+ * otherwise start from slice 0 and fold slices 1..dim-1 with
+ * _mm256_min_ps(out, in) (body) / std::min(out, in) (tail). */
+void orc_reduce_min(const float *x, float *z, size_t outer, size_t dim, size_t inner) {
+    if (inner == 1) {
+        for (size_t o = 0; o < outer; ++o) orc_reduce_min_flat(x + o * dim, z + o, dim);
+        return;
+    }
+    const size_t body = inner - inner % L8;
+    for (size_t o = 0; o < outer; ++o) {
+        float *dst = z + o * inner;
+        const float *src = x + o * dim * inner;
+        memcpy(dst, src, inner * sizeof(float));
+        for (size_t d = 1; d < dim; ++d) {
+            const float *row = src + d * inner;
+            size_t j = 0;
+            for (; j < body; ++j) dst[j] = simd_min(dst[j], row[j]);
+            for (; j < inner; ++j) dst[j] = std_min(dst[j], row[j]);
+        }
+    }
+}
+
+/* --------------------------------------------------------------- argmin */
+
+/* reduce::argmin flat (reduce.cpp:530-557): per 8-block lane argmin, then a
+ * strict '<' against the running best (starting at x[0], index 0). */
+void orc_reduce_argmin_flat(const float *x, int32_t *z, size_t n) {
+    size_t i = 0;
+    float best = x[0];
+    int32_t best_i = 0;
+    for (; i + L8 <= n; i += L8) {
+        const int lane = fold_argmin8(x + i);
+        if (lane < 0) continue;
+        const float cand = x[i + lane];
+        if (cand < best) {
+            best = cand;
+            best_i = (int32_t)(i + lane);
+        }
+    }
+    for (; i < n; ++i) {
+        if (x[i] < best) {
+            best = x[i];
+            best_i = (int32_t)i;
+        }
+    }
+    z[0] = best_i;
+}
+
+/* reduce::argmin axis (reduce.cpp:559-621): inner==1 -> flat per row;
+ * otherwise a running (value, index) per column, replaced on strict '<'. */
+void orc_reduce_argmin(const float *x, int32_t *z, size_t outer, size_t dim, size_t inner) {
+    if (inner == 1) {
+        for (size_t o = 0; o < outer; ++o) orc_reduce_argmin_flat(x + o * dim, z + o, dim);
+        return;
+    }
+    float *best = (float *)malloc(inner * sizeof(float));
+    for (size_t o = 0; o < outer; ++o) {
+        const float *src = x + o * dim * inner;
+        int32_t *dst = z + o * inner;
+        for (size_t j = 0; j < inner; ++j) {
+            best[j] = src[j];
+            dst[j] = 0;
+        }
+        for (size_t d = 1; d < dim; ++d) {
+            const float *row = src + d * inner;
+            for (size_t j = 0; j < inner; ++j) {
+                if (row[j] < best[j]) {
+                    best[j] = row[j];
+                    dst[j] = (int32_t)d;
+                }
+            }
+        }
+    }
+    free(best);
+}
+
+/* ---------------------------------------------------------------- norms */
+
+/* reduce::norm1 flat (reduce.cpp:311-322): 8 lane sums of |x|, fold, tail. */
+void orc_reduce_norm1_flat(const float *x, float *z, size_t n) {
+    float acc[L8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    size_t i = 0;
+    for (; i + L8 <= n; i += L8)
+        for (int l = 0; l < L8; ++l) acc[l] = acc[l] + fabsf(x[i + l]);
+    float r = fold_sum8(acc);
+    for (; i < n; ++i) r += fabsf(x[i]);
+    z[0] = r;
+}
+
+/* reduce::norm1 axis (reduce.cpp:324-367): inner==1 -> flat per row;
+ * otherwise |slice 0|, then add |slice d| in order. */
+void orc_reduce_norm1(const float *x, float *z, size_t outer, size_t dim, size_t inner) {
+    if (inner == 1) {
+        for (size_t o = 0; o < outer; ++o) orc_reduce_norm1_flat(x + o * dim, z + o, dim);
+        return;
+    }
+    for (size_t o = 0; o < outer; ++o) {
+        float *dst = z + o * inner;
+        const float *src = x + o * dim * inner;
+        for (size_t j = 0; j < inner; ++j) dst[j] = fabsf(src[j]);
+        for (size_t d = 1; d < dim; ++d) {
+            const float *row = src + d * inner;
+            for (size_t j = 0; j < inner; ++j) dst[j] = dst[j] + fabsf(row[j]);
+        }
+    }
+}
+
+/* reduce::norm2 flat (reduce.cpp:369-381): lanes acc = fma(v, v, acc)
+ * (fma::add), fold, tail adds the rounded square, then sqrt. */
+void orc_reduce_norm2_flat(const float *x, float *z, size_t n) {
+    float acc[L8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    size_t i = 0;
+    for (; i + L8 <= n; i += L8)
+        for (int l = 0; l < L8; ++l) acc[l] = fmaf(x[i + l], x[i + l], acc[l]);
+    float r = fold_sum8(acc);
+    for (; i < n; ++i) {
+        const float sq = x[i] * x[i];
+        r += sq;
+    }
+    z[0] = sqrtf(r);
+}
+
+/* reduce::norm2 axis (reduce.cpp:383-437): inner==1 -> flat per row;
+ * otherwise slice 0 squared (mul), slices 1.. by fma in the 8-wide body and
+ * rounded square + add in the tail, then sqrt of every output. */
+void orc_reduce_norm2(const float *x, float *z, size_t outer, size_t dim, size_t inner) {
+    if (inner == 1) {
+        for (size_t o = 0; o < outer; ++o) orc_reduce_norm2_flat(x + o * dim, z + o, dim);
+        return;
+    }
+    const size_t body = inner - inner % L8;
+    for (size_t o = 0; o < outer; ++o) {
+        float *dst = z + o * inner;
+        const float *src = x + o * dim * inner;
+        for (size_t j = 0; j < inner; ++j) dst[j] = src[j] * src[j];
+        for (size_t d = 1; d < dim; ++d) {
+            const float *row = src + d * inner;
+            size_t j = 0;
+            for (; j < body; ++j) dst[j] = fmaf(row[j], row[j], dst[j]);
+            for (; j < inner; ++j) {
+                const float sq = row[j] * row[j];
+                dst[j] = dst[j] + sq;
+            }
+        }
+    }
+    for (size_t q = 0; q < outer * inner; ++q) z[q] = sqrtf(z[q]);
+}
+
+/* ------------------------------------------------------------ var, stdv */
+
+/* reduce::var flat (reduce.cpp:86-104): mu = mean flat; lanes accumulate
+ * fma(d, d, acc) with d = x - mu; fold; tail adds the rounded d*d; divide
+ * by N. */
+void orc_reduce_var_flat(const float *x, float *z, size_t n) {
+    float mu;
+    orc_reduce_mean_flat(x, &mu, n);
+    float acc[L8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    size_t i = 0;
+    for (; i + L8 <= n; i += L8)
+        for (int l = 0; l < L8; ++l) {
+            const float d = x[i + l] - mu;
+            acc[l] = fmaf(d, d, acc[l]);
+        }
+    float r = fold_sum8(acc);
+    for (; i < n; ++i) {
+        const float d = x[i] - mu;
+        const float sq = d * d;
+        r += sq;
+    }
+    z[0] = r / (float)n;
+}
+
+/* reduce::var axis (reduce.cpp:106-183).  inner==1: per row, the flat sum
+ * loop, mu = sum / dim (true division), the flat deviation loop, divide by
+ * dim.  Otherwise: mu = mean axis; dst = (x0 - mu)^2 rounded; slices 1.. by
+ * fma in the 8-wide body and rounded square + add in the tail; then the
+ * first floor(total/8)*8 outputs multiply by 1/dim, the rest divide. */
+void orc_reduce_var(const float *x, float *z, size_t outer, size_t dim, size_t inner) {
+    if (inner == 1) {
+        for (size_t o = 0; o < outer; ++o) {
+            const float *src = x + o * dim;
+            float s;
+            orc_reduce_sum_flat(src, &s, dim);
+            const float mu = s / (float)dim;
+            float acc[L8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            size_t i = 0;
+            for (; i + L8 <= dim; i += L8)
+                for (int l = 0; l < L8; ++l) {
+                    const float d = src[i + l] - mu;
+                    acc[l] = fmaf(d, d, acc[l]);
+                }
+            float r = fold_sum8(acc);
+            for (; i < dim; ++i) {
+                const float d = src[i] - mu;
+                const float sq = d * d;
+                r += sq;
+            }
+            z[o] = r / (float)dim;
+        }
+        return;
+    }
+    const size_t total = outer * inner;
+    float *mu = (float *)malloc(total * sizeof(float));
+    orc_reduce_mean(x, mu, outer, dim, inner);
+    const size_t body = inner - inner % L8;
+    for (size_t o = 0; o < outer; ++o) {
+        float *dst = z + o * inner;
+        const float *src = x + o * dim * inner;
+        const float *m = mu + o * inner;
+        for (size_t j = 0; j < inner; ++j) {
+            const float d = src[j] - m[j];
+            dst[j] = d * d;
+        }
+        for (size_t dd = 1; dd < dim; ++dd) {
+            const float *row = src + dd * inner;
+            size_t j = 0;
+            for (; j < body; ++j) {
+                const float d = row[j] - m[j];
+                dst[j] = fmaf(d, d, dst[j]);
+            }
+            for (; j < inner; ++j) {
+                const float d = row[j] - m[j];
+                const float sq = d * d;
+                dst[j] = dst[j] + sq;
+            }
+        }
+    }
+    free(mu);
+    const size_t tbody = total - total % L8;
+    const float scale = 1.0f / (float)dim;
+    size_t q = 0;
+    for (; q < tbody; ++q) z[q] = z[q] * scale;
+    for (; q < total; ++q) z[q] = z[q] / (float)dim;
+}
+
+/* reduce::stdv (reduce.cpp:185-202): sqrt of var, flat and axis. */
+void orc_reduce_stdv_flat(const float *x, float *z, size_t n) {
+    orc_reduce_var_flat(x, z, n);
+    z[0] = sqrtf(z[0]);
+}
+
+void orc_reduce_stdv(const float *x, float *z, size_t outer, size_t dim, size_t inner) {
+    orc_reduce_var(x, z, outer, dim, inner);
+    for (size_t q = 0; q < outer * inner; ++q) z[q] = sqrtf(z[q]);
 }
 
 /* ---------------------------------------------------- elementwise binary */

@@ -54,6 +54,10 @@ def lib() -> ctypes.CDLL:
             "orc_reduce_max": [_F, _F, _SZ, _SZ, _SZ],
             "orc_reduce_argmax_flat": [_F, _I, _SZ],
             "orc_reduce_argmax": [_F, _I, _SZ, _SZ, _SZ],
+            "orc_reduce_argmin_flat": [_F, _I, _SZ],
+            "orc_reduce_argmin": [_F, _I, _SZ, _SZ, _SZ],
+            **{f"orc_reduce_{op}_flat": [_F, _F, _SZ] for op in ("min", "norm1", "norm2", "var", "stdv")},
+            **{f"orc_reduce_{op}": [_F, _F, _SZ, _SZ, _SZ] for op in ("min", "norm1", "norm2", "var", "stdv")},
             "orc_binary": [_F, _F, _F, _SZ, ctypes.c_int],
             "orc_bcast_row": [_F, _F, _F, _SZ, _SZ, ctypes.c_int],
             "orc_bcast_col": [_F, _F, _F, _SZ, _SZ, ctypes.c_int],
@@ -101,9 +105,9 @@ def _c32(a) -> np.ndarray:
 
 def reduce_flat(op: str, x) -> np.ndarray:
     x = _c32(x).ravel()
-    if op == "argmax":
+    if op in ("argmax", "argmin"):
         z = np.zeros(1, np.int32)
-        lib().orc_reduce_argmax_flat(_f(x), _i(z), x.size)
+        getattr(lib(), f"orc_reduce_{op}_flat")(_f(x), _i(z), x.size)
         return z
     z = np.zeros(1, np.float32)
     getattr(lib(), f"orc_reduce_{op}_flat")(_f(x), _f(z), x.size)
@@ -113,9 +117,9 @@ def reduce_flat(op: str, x) -> np.ndarray:
 def reduce_axis(op: str, x, outer: int, dim: int, inner: int) -> np.ndarray:
     x = _c32(x).ravel()
     assert x.size == outer * dim * inner
-    if op == "argmax":
+    if op in ("argmax", "argmin"):
         z = np.zeros(outer * inner, np.int32)
-        lib().orc_reduce_argmax(_f(x), _i(z), outer, dim, inner)
+        getattr(lib(), f"orc_reduce_{op}")(_f(x), _i(z), outer, dim, inner)
         return z
     z = np.zeros(outer * inner, np.float32)
     getattr(lib(), f"orc_reduce_{op}")(_f(x), _f(z), outer, dim, inner)

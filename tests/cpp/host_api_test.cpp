@@ -74,6 +74,15 @@ int main() {
     Dev<float> g(1);
     hip::reduce::max(dx.p, g.p, R * C);
     EXPECT(g.get()[0] == 1000.0f, "global max");
+    hip::reduce::min(dx.p, g.p, R * C);
+    EXPECT(g.get()[0] == -100.0f, "global min");
+    hip::reduce::norm1(dx.p, zr.p, R, C, 1);
+    auto hn = zr.get();
+    for (size_t r = 0; r < R; ++r) {
+        double s = 0;
+        for (size_t c = 0; c < C; ++c) s += std::fabs(x[r * C + c]);
+        EXPECT(hn[r] == static_cast<float>(s), "row norm1 %zu", r);
+    }
 
     // Broadcast::row::add in place, then matrix_t::mul and activation::relu
     std::vector<float> b(C);

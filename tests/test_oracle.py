@@ -451,3 +451,98 @@ def test_gather_vs_numpy_indexing(orc):
     zf, zi = orc.gather(x, bad), orc.gather(xi, bad)
     assert np.isnan(zf[0]) and np.isnan(zf[1]) and zf[2] == x[5]
     assert zi.tolist() == [-(2 ** 31), -(2 ** 31), xi[5]]
+
+
+# ------------------------------------------------- min, argmin, norms, var
+
+@pytest.mark.parametrize("outer,dim,inner", [(1, 1, 1), (1, 13, 1), (7, 100, 1), (1, 9, 5), (4, 33, 17), (2, 8, 8)])
+def test_min_argmin_brute_force(orc, outer, dim, inner):
+    rng = np.random.default_rng(7 * outer + 10 * dim + 100 * inner)
+    x = (rng.integers(-20, 21, size=(outer, dim, inner)) * 0.25).astype(np.float32)
+    assert np.array_equal(orc.reduce_axis("min", x, outer, dim, inner), x.min(axis=1).ravel())
+    assert np.array_equal(orc.reduce_axis("argmin", x, outer, dim, inner),
+                          x.argmin(axis=1).ravel().astype(np.int32))  # first occurrence
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 31, 1000])
+def test_min_argmin_flat_brute_force(orc, n):
+    rng = np.random.default_rng(2000 + n)
+    x = (rng.integers(-5, 6, size=n) * 0.5).astype(np.float32)
+    assert orc.reduce_flat("min", x)[0] == x.min()
+    assert orc.reduce_flat("argmin", x)[0] == int(np.argmin(x))
+
+
+def test_min_start_values(orc):
+    # flat and row forms start from FLT_MAX (reduce.cpp:255, 271), the column
+    # form from slice 0 (reduce.cpp:285-293)
+    inf = f32([np.inf] * 12)
+    assert hexf(orc.reduce_flat("min", inf)[0]) == "0x7f7fffff"
+    assert hexf(orc.reduce_axis("min", inf, 3, 4, 1)[0]) == "0x7f7fffff"
+    assert np.all(np.isposinf(orc.reduce_axis("min", inf, 1, 3, 4)))
+    assert orc.reduce_flat("argmin", inf)[0] == 0
+
+
+@pytest.mark.parametrize("outer,dim,inner", [(1, 7, 3), (2, 5, 9), (1, 257, 33), (3, 64, 17)])
+def test_norm1_axis_matches_numpy_rowwise_order(orc, outer, dim, inner):
+    # |slice 0| then |slice d| added in order: numpy's axis-1 float32 reduce of |x|
+    rng = np.random.default_rng(3 * outer + dim + inner)
+    x = rng.normal(size=(outer, dim, inner)).astype(np.float32)
+    ref = np.add.reduce(np.abs(x), axis=1, dtype=np.float32).ravel()
+    assert np.array_equal(orc.reduce_axis("norm1", x, outer, dim, inner), ref)
+
+
+@pytest.mark.parametrize("outer,dim,inner", [(1, 1000, 1), (5, 9, 1), (2, 3, 7), (1, 77, 12)])
+def test_norms_small_integers_exact(orc, outer, dim, inner):
+    # |x| and x*x of small integers and their sums are exact in float32, in any order
+    rng = np.random.default_rng(11 + outer + dim + inner)
+    x = rng.integers(-40, 41, size=(outer, dim, inner)).astype(np.float32)
+    xi = x.astype(np.int64)
+    n1 = np.abs(xi).sum(axis=1).ravel().astype(np.float32)
+    n2 = np.sqrt((xi * xi).sum(axis=1).ravel().astype(np.float32))
+    assert np.array_equal(orc.reduce_axis("norm1", x, outer, dim, inner), n1)
+    assert np.array_equal(orc.reduce_axis("norm2", x, outer, dim, inner), n2)
+    if inner == 1 and outer == 1:
+        assert orc.reduce_flat("norm1", x)[0] == n1[0]
+        assert orc.reduce_flat("norm2", x)[0] == n2[0]
+
+
+@pytest.mark.parametrize("n", [5, 4099, 1 << 16])
+def test_norms_vs_float64(orc, n):
+    x = np.random.default_rng(n).normal(size=n).astype(np.float32)
+    d = x.astype(np.float64)
+    assert abs(orc.reduce_flat("norm1", x)[0] - np.abs(d).sum()) <= 1e-5 * np.abs(d).sum()
+    assert abs(orc.reduce_flat("norm2", x)[0] - np.sqrt((d * d).sum())) <= 1e-5 * np.sqrt((d * d).sum())
+
+
+def test_var_axis_reciprocal_body_division_tail(orc):
+    # 9 columns, each (0.5, 2.5, 3.0): the column mean is exactly 2 and the
+    # squared deviations sum to exactly 3.5.  reduce.cpp:173-182 multiplies
+    # the first 8 outputs by rn(1/3): 3.5 * 0.333333343 rounds to 0x3f955556;
+    # the 9th divides: rn(3.5/3) = 0x3f955555.  Rows divide (reduce.cpp:135).
+    x = np.repeat(f32([0.5, 2.5, 3.0]), 9).reshape(3, 9)
+    z = orc.reduce_axis("var", x, 1, 3, 9)
+    assert all(hexf(v) == "0x3f955556" for v in z[:8]) and hexf(z[8]) == "0x3f955555"
+    zr = orc.reduce_axis("var", f32([0.5, 2.5, 3.0] * 4), 4, 3, 1)
+    assert all(hexf(v) == "0x3f955555" for v in zr)
+    assert hexf(orc.reduce_flat("var", f32([0.5, 2.5, 3.0]))[0]) == "0x3f955555"
+    s = orc.reduce_axis("stdv", x, 1, 3, 9)
+    assert np.array_equal(s, np.sqrt(z))  # stdv = sqrt(var), reduce.cpp:190-202
+
+
+@pytest.mark.parametrize("outer,dim,inner", [(1, 4099, 1), (3, 1000, 1), (1, 500, 40), (2, 37, 9)])
+def test_var_stdv_vs_float64(orc, outer, dim, inner):
+    rng = np.random.default_rng(outer + dim + inner)
+    x = rng.normal(3.0, 2.0, size=(outer, dim, inner)).astype(np.float32)
+    d = x.astype(np.float64)
+    v = d.var(axis=1).ravel()  # population variance
+    assert np.all(np.abs(orc.reduce_axis("var", x, outer, dim, inner) - v) <= 1e-5 * v)
+    assert np.all(np.abs(orc.reduce_axis("stdv", x, outer, dim, inner) - np.sqrt(v)) <= 1e-5 * np.sqrt(v))
+    f = x.ravel()
+    assert abs(orc.reduce_flat("var", f)[0] - f.astype(np.float64).var()) <= 1e-5 * f.astype(np.float64).var()
+
+
+def test_var_closed_forms(orc):
+    assert orc.reduce_flat("var", f32([7.25] * 1001))[0] == 0.0  # constant
+    assert orc.reduce_flat("var", f32([-3.0, 3.0] * 64))[0] == 9.0  # +-c: c^2
+    assert orc.reduce_flat("stdv", f32([-3.0, 3.0] * 64))[0] == 3.0
+    assert np.isnan(orc.reduce_flat("var", np.zeros(0, np.float32))[0])  # 0/0
