@@ -256,8 +256,8 @@ __global__ void k_fill_f32(float *z, float v) { *z = v; }
 
 constexpr unsigned kTargetBlocks = 2048;
 
-template <class Op>
-int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t s) {
+template <class Op, int UNRV = 8>
+int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t s, size_t seg_floats = 0) {
     using T = typename Op::T;
     hipStream_t hs = reinterpret_cast<hipStream_t>(s);
     const bool vec = aligned16(x) && dim % 4 == 0;
@@ -271,6 +271,7 @@ int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t 
         if (segs == 0) segs = 1;
     }
     size_t seg_len = (dim + segs - 1) / segs;
+    if (seg_floats) seg_len = seg_floats;
     seg_len = (seg_len + 1023) / 1024 * 1024;
     segs = seg_len ? (dim + seg_len - 1) / seg_len : 1;
     if (segs == 0) segs = 1;
@@ -289,8 +290,8 @@ int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t 
     }
     const unsigned nb = static_cast<unsigned>(blocks);
     const size_t per_thread = seg_len / (4 * kBlock);  // float4 loads per thread
-    if (vec && per_thread >= 8)
-        hipLaunchKernelGGL((k_rows<Op, true, 8>), dim3(nb), dim3(kBlock), 0, hs, x, dim,
+    if (vec && per_thread >= UNRV)
+        hipLaunchKernelGGL((k_rows<Op, true, UNRV>), dim3(nb), dim3(kBlock), 0, hs, x, dim,
                            static_cast<unsigned>(segs), seg_len, part, counters, out);
     else if (vec)
         hipLaunchKernelGGL((k_rows<Op, true, 4>), dim3(nb), dim3(kBlock), 0, hs, x, dim,
@@ -320,7 +321,7 @@ ColPlan col_plan(size_t tiles, size_t dim) {
     return p;
 }
 
-template <class Op>
+template <class Op, int UNRC = 8>
 int run_cols_plan(const float *x, size_t outer, size_t dim, size_t inner, OutDesc out, ColPlan plan,
                   cxm_stream_t s) {
     using T = typename Op::T;
@@ -351,10 +352,10 @@ int run_cols_plan(const float *x, size_t outer, size_t dim, size_t inner, OutDes
     hipLaunchKernelGGL((k_cols<Op, VEC_, UNR_, NW_>), dim3(nb), dim3(NW_ * kWave), 0, hs, x, dim, inner, \
                        nt, nc, rpc, plan.tile_major, part, counters, out)
     if (plan.nw == 16) {
-        if (vec) CXM_COLS(true, 8, 16);
+        if (vec) CXM_COLS(true, UNRC, 16);
         else CXM_COLS(false, 1, 16);
     } else {
-        if (vec) CXM_COLS(true, 8, 4);
+        if (vec) CXM_COLS(true, UNRC, 4);
         else CXM_COLS(false, 1, 4);
     }
 #undef CXM_COLS

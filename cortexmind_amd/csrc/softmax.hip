@@ -7,9 +7,10 @@
 //       (broadcast.cpp:292-304), e = exp(z), s = reduce::sum(e)
 //       (reduce.cpp:17-28), y = Broadcast::col::div(e, s) (broadcast.cpp:320-332)
 //       or y = z - log(s),
-// and these kernels compute exactly that per element (z = x - m rounded, then
-// expf, then one division or one subtraction); only the order in which s is
-// summed differs.
+// and these kernels compute that per element (z = x - m rounded, then expf,
+// then a subtraction of log(s), or a product with the correctly rounded 1/s
+// in place of the division: at most one rounding apart); the order in
+// which s is summed differs.
 //
 // Three kernel families by row length:
 //  * wave per row, row in registers (cols <= 4096, cols % 4 == 0): one pass
@@ -55,7 +56,12 @@ __global__ __launch_bounds__(kBlock) void k_sm_fwd_wave(const float *__restrict_
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         v[k].x = v[k].x - m; v[k].y = v[k].y - m; v[k].z = v[k].z - m; v[k].w = v[k].w - m;
-        s += (expf(v[k].x) + expf(v[k].y)) + (expf(v[k].z) + expf(v[k].w));
+        if constexpr (LOG) {
+            s += (expf(v[k].x) + expf(v[k].y)) + (expf(v[k].z) + expf(v[k].w));
+        } else {  // keep e = exp(z) for the output
+            v[k] = make_float4(expf(v[k].x), expf(v[k].y), expf(v[k].z), expf(v[k].w));
+            s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+        }
     }
     s = wave_reduce<SumOp>(s);
     if constexpr (LOG) {
@@ -67,12 +73,11 @@ __global__ __launch_bounds__(kBlock) void k_sm_fwd_wave(const float *__restrict_
                 st4_stream(yr + 4 * i, make_float4(v[k].x - ls, v[k].y - ls, v[k].z - ls, v[k].w - ls));
         }
     } else {
+        const float inv = 1.0f / s;  // e * rn(1/s): one rounding from e / s
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const size_t i = static_cast<size_t>(k) * kWave + lane;
-            if (i < c4)
-                st4_stream(yr + 4 * i, make_float4(expf(v[k].x) / s, expf(v[k].y) / s,
-                                                   expf(v[k].z) / s, expf(v[k].w) / s));
+            if (i < c4) st4_stream(yr + 4 * i, make_float4(v[k].x * inv, v[k].y * inv, v[k].z * inv, v[k].w * inv));
         }
     }
 }
@@ -122,38 +127,62 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_wave(const float *__restrict_
 
 // ------------------------------------------------------------ split rows
 
-constexpr int kSegNV = 4;                       // float4 per thread per segment
-constexpr size_t kSegLen = kBlock * 4 * kSegNV; // 4096 floats
+// Segment = NV float4 per thread of a 256-thread workgroup (1024*NV floats).
+constexpr int kSegNV = 4;
 
 struct MS {
     float m, s;
 };
-
 // Pass 1 forward: per (row, segment) the segment max m_b and
-// s_b = sum exp(x - m_b).  grid = rows * segs.
+// s_b = sum exp(x - m_b).  A segment is NV float4 per thread, streamed in
+// chunks of 4 float4 with the next chunk's loads in flight while the
+// current one is folded into the thread's running (max, sum) -- the
+// online rescaling s = s*exp(m - m') + sum exp(x - m') of Milakov and
+// Gimelshein (2018).  Then a block max, one rescale per thread, and a block
+// sum.  grid = rows * segs.
+template <int NV>
 __global__ __launch_bounds__(kBlock) void k_sm_fwd_part(const float *__restrict__ x, size_t cols,
                                                         unsigned segs, MS *__restrict__ part) {
+    constexpr size_t L = kBlock * 4 * NV;
+    constexpr int C = NV < 4 ? NV : 4;  // float4 per thread per chunk
+    static_assert(NV % C == 0, "segment = whole chunks");
     __shared__ float lds[kWavesPerBlock];
     const size_t row = blockIdx.x / segs;
     const unsigned seg = blockIdx.x - static_cast<unsigned>(row) * segs;
-    const float *__restrict__ xs = x + row * cols + static_cast<size_t>(seg) * kSegLen;
-    const size_t n4 = (cols - static_cast<size_t>(seg) * kSegLen) / 4;  // float4 left in the row
-    float4 v[kSegNV];
+    const float *__restrict__ xs = x + row * cols + static_cast<size_t>(seg) * L;
+    const size_t n4 = (cols - static_cast<size_t>(seg) * L) / 4;  // float4 left in the row
+    const float4 ninf = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    float4 cur[C], nxt[C];
 #pragma unroll
-    for (int k = 0; k < kSegNV; ++k) {
+    for (int k = 0; k < C; ++k) {
         const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
-        v[k] = i < n4 ? ld4(xs + 4 * i) : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        cur[k] = i < n4 ? ld4(xs + 4 * i) : ninf;
     }
-    float m = kLowest;
+    float m = kLowest, s = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kSegNV; ++k) m = vmax(vmax(vmax(vmax(m, v[k].x), v[k].y), v[k].z), v[k].w);
-    m = block_reduce<MaxOp, kBlock>(m, lds);
-    float s = 0.0f;
+    for (int c = 0; c < NV / C; ++c) {
+        if (c + 1 < NV / C) {
 #pragma unroll
-    for (int k = 0; k < kSegNV; ++k)
-        s += (expf(v[k].x - m) + expf(v[k].y - m)) + (expf(v[k].z - m) + expf(v[k].w - m));
-    s = block_reduce<SumOp, kBlock>(s, lds);
-    if (threadIdx.x == 0) part[blockIdx.x] = MS{m, s};
+            for (int k = 0; k < C; ++k) {
+                const size_t i = static_cast<size_t>((c + 1) * C + k) * kBlock + threadIdx.x;
+                nxt[k] = i < n4 ? ld4(xs + 4 * i) : ninf;
+            }
+        }
+        float mc = m;
+#pragma unroll
+        for (int k = 0; k < C; ++k) mc = vmax(vmax(vmax(vmax(mc, cur[k].x), cur[k].y), cur[k].z), cur[k].w);
+        float sc = s * expf(m - mc);
+#pragma unroll
+        for (int k = 0; k < C; ++k)
+            sc += (expf(cur[k].x - mc) + expf(cur[k].y - mc)) + (expf(cur[k].z - mc) + expf(cur[k].w - mc));
+        m = mc;
+        s = sc;
+#pragma unroll
+        for (int k = 0; k < C; ++k) cur[k] = nxt[k];
+    }
+    const float M = block_reduce<MaxOp, kBlock>(m, lds);
+    const float S = block_reduce<SumOp, kBlock>(s * expf(m - M), lds);
+    if (threadIdx.x == 0) part[blockIdx.x] = MS{M, S};
 }
 
 // Row max M and S = sum_b s_b * exp(m_b - M) from the row's partials, in a
@@ -168,94 +197,124 @@ __device__ __forceinline__ MS combine_row(const MS *__restrict__ p, unsigned seg
     return MS{m, s};
 }
 
-template <bool LOG>
+// Pass 2 forward: y = exp(x - M) * (1/S), or (x - M) - log(S).  The
+// correctly rounded reciprocal times e differs from e / S by at most one
+// rounding, and saves the per-element division.  Chunks of 4 float4 per
+// thread, the next chunk's loads in flight while the current one is
+// written.
+template <int NV, bool LOG>
 __global__ __launch_bounds__(kBlock) void k_sm_fwd_apply(const float *__restrict__ x,
                                                          float *__restrict__ y, size_t cols,
                                                          unsigned segs, const MS *__restrict__ part) {
+    constexpr size_t L = kBlock * 4 * NV;
+    constexpr int C = NV < 4 ? NV : 4;
+    static_assert(NV % C == 0, "segment = whole chunks");
     __shared__ float lds[kWavesPerBlock];
     const size_t row = blockIdx.x / segs;
     const unsigned seg = blockIdx.x - static_cast<unsigned>(row) * segs;
-    const MS t = combine_row(part + row * segs, segs, lds);
-    const size_t base = row * cols + static_cast<size_t>(seg) * kSegLen;
-    const size_t n4 = (cols - static_cast<size_t>(seg) * kSegLen) / 4;
-    float4 v[kSegNV];
+    const size_t base = row * cols + static_cast<size_t>(seg) * L;
+    const size_t n4 = (cols - static_cast<size_t>(seg) * L) / 4;
+    float4 cur[C], nxt[C];
 #pragma unroll
-    for (int k = 0; k < kSegNV; ++k) {
+    for (int k = 0; k < C; ++k) {
         const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
-        if (i < n4) v[k] = ld4_stream(x + base + 4 * i);
+        if (i < n4) cur[k] = ld4_stream(x + base + 4 * i);
     }
+    const MS t = combine_row(part + row * segs, segs, lds);
     const float ls = LOG ? logf(t.s) : 0.0f;
+    const float inv = LOG ? 0.0f : 1.0f / t.s;
 #pragma unroll
-    for (int k = 0; k < kSegNV; ++k) {
-        const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
-        if (i >= n4) continue;
-        float4 z;
-        z.x = v[k].x - t.m; z.y = v[k].y - t.m; z.z = v[k].z - t.m; z.w = v[k].w - t.m;
-        float4 o;
-        if constexpr (LOG) {
-            o = make_float4(z.x - ls, z.y - ls, z.z - ls, z.w - ls);
-        } else {
-            o = make_float4(expf(z.x) / t.s, expf(z.y) / t.s, expf(z.z) / t.s, expf(z.w) / t.s);
+    for (int c = 0; c < NV / C; ++c) {
+        if (c + 1 < NV / C) {
+#pragma unroll
+            for (int k = 0; k < C; ++k) {
+                const size_t i = static_cast<size_t>((c + 1) * C + k) * kBlock + threadIdx.x;
+                if (i < n4) nxt[k] = ld4_stream(x + base + 4 * i);
+            }
         }
-        st4_stream(y + base + 4 * i, o);
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            const size_t i = static_cast<size_t>(c * C + k) * kBlock + threadIdx.x;
+            if (i >= n4) continue;
+            float4 z;
+            z.x = cur[k].x - t.m; z.y = cur[k].y - t.m; z.z = cur[k].z - t.m; z.w = cur[k].w - t.m;
+            float4 o;
+            if constexpr (LOG) {
+                o = make_float4(z.x - ls, z.y - ls, z.z - ls, z.w - ls);
+            } else {
+                o = make_float4(expf(z.x) * inv, expf(z.y) * inv, expf(z.z) * inv, expf(z.w) * inv);
+            }
+            st4_stream(y + base + 4 * i, o);
+        }
+#pragma unroll
+        for (int k = 0; k < C; ++k) cur[k] = nxt[k];
     }
 }
 
 // Pass 1 backward: per (row, segment) partial of sum(dy*y) or sum(dy).
-template <bool LOG>
+template <int NV, bool LOG>
 __global__ __launch_bounds__(kBlock) void k_sm_bwd_part(const float *__restrict__ y,
                                                         const float *__restrict__ dy, size_t cols,
                                                         unsigned segs, float *__restrict__ part) {
+    constexpr size_t L = kBlock * 4 * NV;
     __shared__ float lds[kWavesPerBlock];
     const size_t row = blockIdx.x / segs;
     const unsigned seg = blockIdx.x - static_cast<unsigned>(row) * segs;
-    const size_t base = row * cols + static_cast<size_t>(seg) * kSegLen;
-    const size_t n4 = (cols - static_cast<size_t>(seg) * kSegLen) / 4;
+    const size_t base = row * cols + static_cast<size_t>(seg) * L;
+    const size_t n4 = (cols - static_cast<size_t>(seg) * L) / 4;
+    float4 g[NV], yy[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
+        const bool in = i < n4;
+        g[k] = in ? ld4(dy + base + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (!LOG) yy[k] = in ? ld4(y + base + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     float r = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kSegNV; ++k) {
-        const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
-        if (i < n4) {
-            const float4 g = ld4(dy + base + 4 * i);
-            if constexpr (LOG) {
-                r += (g.x + g.y) + (g.z + g.w);
-            } else {
-                const float4 yy = ld4(y + base + 4 * i);
-                r += (g.x * yy.x + g.y * yy.y) + (g.z * yy.z + g.w * yy.w);
-            }
-        }
+    for (int k = 0; k < NV; ++k) {
+        if constexpr (LOG) r += (g[k].x + g[k].y) + (g[k].z + g[k].w);
+        else r += (g[k].x * yy[k].x + g[k].y * yy[k].y) + (g[k].z * yy[k].z + g[k].w * yy[k].w);
     }
     r = block_reduce<SumOp, kBlock>(r, lds);
     if (threadIdx.x == 0) part[blockIdx.x] = r;
 }
 
-template <bool LOG>
+template <int NV, bool LOG>
 __global__ __launch_bounds__(kBlock) void k_sm_bwd_apply(const float *__restrict__ y,
                                                          const float *__restrict__ dy,
                                                          float *__restrict__ dx, size_t cols,
                                                          unsigned segs,
                                                          const float *__restrict__ part) {
+    constexpr size_t L = kBlock * 4 * NV;
     __shared__ float lds[kWavesPerBlock];
     const size_t row = blockIdx.x / segs;
     const unsigned seg = blockIdx.x - static_cast<unsigned>(row) * segs;
     float r = 0.0f;
     for (unsigned b = threadIdx.x; b < segs; b += kBlock) r += part[row * segs + b];
     r = block_reduce<SumOp, kBlock>(r, lds);
-    const size_t base = row * cols + static_cast<size_t>(seg) * kSegLen;
-    const size_t n4 = (cols - static_cast<size_t>(seg) * kSegLen) / 4;
+    const size_t base = row * cols + static_cast<size_t>(seg) * L;
+    const size_t n4 = (cols - static_cast<size_t>(seg) * L) / 4;
+    float4 yy[NV], g[NV];
 #pragma unroll
-    for (int k = 0; k < kSegNV; ++k) {
+    for (int k = 0; k < NV; ++k) {
+        const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
+        if (i < n4) {
+            yy[k] = ld4_stream(y + base + 4 * i);
+            g[k] = ld4_stream(dy + base + 4 * i);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
         const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
         if (i >= n4) continue;
-        const float4 yy = ld4_stream(y + base + 4 * i);
-        const float4 g = ld4_stream(dy + base + 4 * i);
         float4 o;
         if constexpr (LOG) {
-            o.x = g.x - expf(yy.x) * r; o.y = g.y - expf(yy.y) * r;
-            o.z = g.z - expf(yy.z) * r; o.w = g.w - expf(yy.w) * r;
+            o.x = g[k].x - expf(yy[k].x) * r; o.y = g[k].y - expf(yy[k].y) * r;
+            o.z = g[k].z - expf(yy[k].z) * r; o.w = g[k].w - expf(yy[k].w) * r;
         } else {
-            o.x = yy.x * (g.x - r); o.y = yy.y * (g.y - r);
-            o.z = yy.z * (g.z - r); o.w = yy.w * (g.w - r);
+            o.x = yy[k].x * (g[k].x - r); o.y = yy[k].y * (g[k].y - r);
+            o.z = yy[k].z * (g[k].z - r); o.w = yy[k].w * (g[k].w - r);
         }
         st4_stream(dx + base + 4 * i, o);
     }
@@ -389,6 +448,53 @@ int sm_bwd_wave(const float *y, const float *dy, float *dx, size_t rows, size_t 
 // Long rows: split when a row exceeds the wave kernel's register capacity.
 bool use_split(size_t cols) { return cols > kWaveRowMax; }
 
+template <int NV>
+int sm_fwd_split(const float *x, float *y, size_t rows, size_t cols, int log_mode, cxm_stream_t st) {
+    constexpr size_t L = kBlock * 4 * NV;
+    const size_t segs = (cols + L - 1) / L;
+    if (rows * segs > 0x7fffffffu) return CXM_E_TOO_LARGE;
+    Workspace ws;
+    int rc = get_workspace(st, 0, rows * segs * sizeof(MS), &ws);
+    if (rc) return rc;
+    MS *part = static_cast<MS *>(ws.scratch);
+    const dim3 grid(static_cast<unsigned>(rows * segs));
+    hipStream_t s = hs(st);
+    hipLaunchKernelGGL(k_sm_fwd_part<NV>, grid, dim3(kBlock), 0, s, x, cols, static_cast<unsigned>(segs), part);
+    if ((rc = launch_status())) return rc;
+    if (log_mode)
+        hipLaunchKernelGGL((k_sm_fwd_apply<NV, true>), grid, dim3(kBlock), 0, s, x, y, cols,
+                           static_cast<unsigned>(segs), part);
+    else
+        hipLaunchKernelGGL((k_sm_fwd_apply<NV, false>), grid, dim3(kBlock), 0, s, x, y, cols,
+                           static_cast<unsigned>(segs), part);
+    return launch_status();
+}
+
+template <int NV>
+int sm_bwd_split(const float *y, const float *dy, float *dx, size_t rows, size_t cols, int log_mode,
+                 cxm_stream_t st) {
+    constexpr size_t L = kBlock * 4 * NV;
+    const size_t segs = (cols + L - 1) / L;
+    if (rows * segs > 0x7fffffffu) return CXM_E_TOO_LARGE;
+    Workspace ws;
+    int rc = get_workspace(st, 0, rows * segs * sizeof(float), &ws);
+    if (rc) return rc;
+    float *part = static_cast<float *>(ws.scratch);
+    const dim3 grid(static_cast<unsigned>(rows * segs));
+    hipStream_t s = hs(st);
+    const unsigned sg = static_cast<unsigned>(segs);
+    if (log_mode) {
+        hipLaunchKernelGGL((k_sm_bwd_part<NV, true>), grid, dim3(kBlock), 0, s, y, dy, cols, sg, part);
+        if ((rc = launch_status())) return rc;
+        hipLaunchKernelGGL((k_sm_bwd_apply<NV, true>), grid, dim3(kBlock), 0, s, y, dy, dx, cols, sg, part);
+    } else {
+        hipLaunchKernelGGL((k_sm_bwd_part<NV, false>), grid, dim3(kBlock), 0, s, y, dy, cols, sg, part);
+        if ((rc = launch_status())) return rc;
+        hipLaunchKernelGGL((k_sm_bwd_apply<NV, false>), grid, dim3(kBlock), 0, s, y, dy, dx, cols, sg, part);
+    }
+    return launch_status();
+}
+
 int softmax_fwd(const float *x, float *y, size_t rows, size_t cols, int log_mode, cxm_stream_t st) {
     if (!x || !y || (log_mode != 0 && log_mode != 1)) return CXM_E_INVALID;
     if (rows == 0 || cols == 0) return CXM_OK;
@@ -402,22 +508,7 @@ int softmax_fwd(const float *x, float *y, size_t rows, size_t cols, int log_mode
     }
     if (!use_split(cols))
         return log_mode ? sm_fwd_wave<true>(x, y, rows, cols, s) : sm_fwd_wave<false>(x, y, rows, cols, s);
-    const size_t segs = (cols + kSegLen - 1) / kSegLen;
-    if (rows * segs > 0x7fffffffu) return CXM_E_TOO_LARGE;
-    Workspace ws;
-    int rc = get_workspace(st, 0, rows * segs * sizeof(MS), &ws);
-    if (rc) return rc;
-    MS *part = static_cast<MS *>(ws.scratch);
-    const dim3 grid(static_cast<unsigned>(rows * segs));
-    hipLaunchKernelGGL(k_sm_fwd_part, grid, dim3(kBlock), 0, s, x, cols, static_cast<unsigned>(segs), part);
-    if ((rc = launch_status())) return rc;
-    if (log_mode)
-        hipLaunchKernelGGL(k_sm_fwd_apply<true>, grid, dim3(kBlock), 0, s, x, y, cols,
-                           static_cast<unsigned>(segs), part);
-    else
-        hipLaunchKernelGGL(k_sm_fwd_apply<false>, grid, dim3(kBlock), 0, s, x, y, cols,
-                           static_cast<unsigned>(segs), part);
-    return launch_status();
+    return sm_fwd_split<kSegNV>(x, y, rows, cols, log_mode, st);
 }
 
 int softmax_bwd(const float *y, const float *dy, float *dx, size_t rows, size_t cols, int log_mode,
@@ -435,27 +526,7 @@ int softmax_bwd(const float *y, const float *dy, float *dx, size_t rows, size_t 
     if (!use_split(cols))
         return log_mode ? sm_bwd_wave<true>(y, dy, dx, rows, cols, s)
                         : sm_bwd_wave<false>(y, dy, dx, rows, cols, s);
-    const size_t segs = (cols + kSegLen - 1) / kSegLen;
-    if (rows * segs > 0x7fffffffu) return CXM_E_TOO_LARGE;
-    Workspace ws;
-    int rc = get_workspace(st, 0, rows * segs * sizeof(float), &ws);
-    if (rc) return rc;
-    float *part = static_cast<float *>(ws.scratch);
-    const dim3 grid(static_cast<unsigned>(rows * segs));
-    if (log_mode) {
-        hipLaunchKernelGGL(k_sm_bwd_part<true>, grid, dim3(kBlock), 0, s, y, dy, cols,
-                           static_cast<unsigned>(segs), part);
-        if ((rc = launch_status())) return rc;
-        hipLaunchKernelGGL(k_sm_bwd_apply<true>, grid, dim3(kBlock), 0, s, y, dy, dx, cols,
-                           static_cast<unsigned>(segs), part);
-    } else {
-        hipLaunchKernelGGL(k_sm_bwd_part<false>, grid, dim3(kBlock), 0, s, y, dy, cols,
-                           static_cast<unsigned>(segs), part);
-        if ((rc = launch_status())) return rc;
-        hipLaunchKernelGGL(k_sm_bwd_apply<false>, grid, dim3(kBlock), 0, s, y, dy, dx, cols,
-                           static_cast<unsigned>(segs), part);
-    }
-    return launch_status();
+    return sm_bwd_split<kSegNV>(y, dy, dx, rows, cols, log_mode, st);
 }
 
 }  // namespace
