@@ -35,6 +35,15 @@ constexpr int SLOTS = BM * BK / 4 / kGemmThreads;  // float4 groups per thread p
 constexpr int kColTileThin = 256;  // m columns per workgroup of the thin TN kernel
 
 
+// Workgroups are dispatched to the 8 XCDs round-robin (workgroup b runs on
+// XCD b % 8).  Renumbering b so that each XCD gets one contiguous eighth of
+// the row-major tile order makes the tiles sharing an XCD's L2 share A rows
+// (and B columns), instead of every XCD touching every row block.
+__device__ __forceinline__ unsigned xcd_remap(unsigned b, unsigned g) {
+    if (g % 8 != 0) return b;
+    return (b % 8) * (g / 8) + b / 8;
+}
+
 __device__ __forceinline__ void store_epi(const Epilogue &e, float *C, size_t row, size_t col, size_t N,
                                           float v) {
     float *p = C + row * N + col;
@@ -135,7 +144,75 @@ __device__ __forceinline__ void store_b(float (*Bs)[BN + PAD], int slot, float4 
     }
 }
 
-template <bool TA, bool TB, bool VA, bool VB>
+// Writes the workgroup's 128x128 tile from the accumulators: directly (with
+// the epilogue) when K is not split; otherwise the split's partial goes to
+// the workspace and the last workgroup of the tile adds the partials in
+// split order, then applies the epilogue.
+template <int WI_, int WJ_>
+__device__ __forceinline__ void gemm_epilogue(floatx16 (&acc)[WI_][WJ_], float *__restrict__ C, size_t M, size_t N,
+                                              size_t m0, size_t n0, unsigned tile, unsigned split, unsigned splits,
+                                              int wm, int wn, int lhi, int l32, const Epilogue &epi,
+                                              float *__restrict__ part, unsigned *__restrict__ counters, int *flag) {
+    // Output element of accumulator (i, j, r) for this lane.
+    auto out_row = [&](int i, int r) { return wm * 32 * WI_ + i * 32 + 8 * (r / 4) + 4 * lhi + (r % 4); };
+    auto out_col = [&](int j) { return wn * 32 * WJ_ + j * 32 + l32; };
+
+    if (splits == 1) {
+#pragma unroll
+        for (int i = 0; i < WI_; ++i)
+#pragma unroll
+            for (int j = 0; j < WJ_; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const size_t row = m0 + out_row(i, r), col = n0 + out_col(j);
+                    if (row < M && col < N) store_epi(epi, C, row, col, N, acc[i][j][r]);
+                }
+        return;
+    }
+
+    float *my = part + (static_cast<size_t>(tile) * splits + split) * (BM * BN);
+#pragma unroll
+    for (int i = 0; i < WI_; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ_; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) st_dev(&my[out_row(i, r) * BN + out_col(j)], acc[i][j][r]);
+    if (!last_block_ticket(ctr(counters, tile), splits, flag)) return;
+    // Sum the splits in split order; each round issues this lane's 64 loads together.
+    const float *tp = part + static_cast<size_t>(tile) * splits * (BM * BN);
+#pragma unroll
+    for (int i = 0; i < WI_; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ_; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (unsigned s = 0; s < splits; ++s) {
+        float v[WI_][WJ_][16];
+#pragma unroll
+        for (int i = 0; i < WI_; ++i)
+#pragma unroll
+            for (int j = 0; j < WJ_; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) v[i][j][r] = ld_dev(&tp[s * (BM * BN) + out_row(i, r) * BN + out_col(j)]);
+#pragma unroll
+        for (int i = 0; i < WI_; ++i)
+#pragma unroll
+            for (int j = 0; j < WJ_; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + v[i][j][r];
+    }
+#pragma unroll
+    for (int i = 0; i < WI_; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ_; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const size_t row = m0 + out_row(i, r), col = n0 + out_col(j);
+                if (row < M && col < N) store_epi(epi, C, row, col, N, acc[i][j][r]);
+            }
+}
+
+template <bool TA, bool TB, bool VA, bool VB, bool XCDMAP = false>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm(const float *__restrict__ A, const float *__restrict__ B,
                                                  float *__restrict__ C, size_t M, size_t N, size_t K,
                                                  unsigned tiles_n, unsigned splits, size_t kper,
@@ -145,8 +222,9 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(const float *__restrict__
     __shared__ float Bs[2][BK][BN + PAD];
     __shared__ int flag;
 
-    const unsigned tile = blockIdx.x / splits;
-    const unsigned split = blockIdx.x - tile * splits;
+    const unsigned wg = XCDMAP ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x;
+    const unsigned tile = wg / splits;
+    const unsigned split = wg - tile * splits;
     const size_t m0 = static_cast<size_t>(tile / tiles_n) * BM;
     const size_t n0 = static_cast<size_t>(tile % tiles_n) * BN;
     const size_t kbeg = static_cast<size_t>(split) * kper;
@@ -239,63 +317,339 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(const float *__restrict__
         buf ^= 1;
     }
 
-    // Output element of accumulator (i, j, r) for this lane.
-    auto out_row = [&](int i, int r) { return wm * 64 + i * 32 + 8 * (r / 4) + 4 * lhi + (r % 4); };
-    auto out_col = [&](int j) { return wn * 32 + j * 32 + l32; };
+    gemm_epilogue<WI, WJ>(acc, C, M, N, m0, n0, tile, split, splits, wm, wn, lhi, l32, epi, part, counters, &flag);
+}
 
-    if (splits == 1) {
-#pragma unroll
-        for (int i = 0; i < WI; ++i)
-#pragma unroll
-            for (int j = 0; j < WJ; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const size_t row = m0 + out_row(i, r), col = n0 + out_col(j);
-                    if (row < M && col < N) store_epi(epi, C, row, col, N, acc[i][j][r]);
-                }
-        return;
+// ------------------------------------------------ k-contiguous variant
+//
+// Same workgroup and wave tiling, but both LDS tiles are stored with k
+// contiguous (As[m][k], Bs[n][k], row stride KP = 36 floats) so that one
+// ds_read_b128 gives a lane the operands of four MFMAs.  The k order inside
+// an 8-wide k block is permuted identically for A and B: in MFMA j of the
+// block, lanes 0-31 supply k = kb + j and lanes 32-63 k = kb + 4 + j, so the
+// four MFMAs still cover each k of the block exactly once.  With the stride
+// of 36 floats, the 16-lane phases of a b128 read hit 16 distinct 4-bank
+// groups.
+
+// Staging of one operand tile (128 rows r = m or n, BK = 32 k) through
+// registers into the k-contiguous LDS tile Xs[r][k].
+//  * KC (stored X[R][Kd], k contiguous): slot -> row r = slot / 8, k quad
+//    q = slot % 8; one 128-bit load and one 128-bit LDS write.
+//  * otherwise (stored X[Kd][R]): slot -> 4 consecutive rows 4*rq.. of one
+//    k; one 128-bit load along r (8 lanes cover 128 contiguous bytes) and
+//    four scalar LDS writes.  The lane bits are arranged (rq low 3 bits,
+//    k low 3 bits, then the high bits) so that a write instruction meets
+//    at most 2-way bank conflicts with the 36-float row stride.
+template <bool KC, int BKT>
+struct Stage {
+    static constexpr int KPT = BKT + 4;  // LDS row stride
+    int r, k;  // KC: row, first k of the quad; else: first row of the quad, k
+    __device__ __forceinline__ void init(int slot) {
+        if constexpr (KC) {
+            r = slot / (BKT / 4);
+            k = (slot % (BKT / 4)) * 4;
+        } else {
+            r = 4 * ((slot & 7) + 8 * ((slot >> 6) & 3));
+            k = ((slot >> 3) & 7) + 8 * (slot >> 8);
+        }
     }
+    template <bool V>
+    __device__ __forceinline__ float4 load(const float *__restrict__ X, size_t r0, size_t k0, size_t R,
+                                           size_t Kd) const {
+        const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (KC) {
+            const size_t rg = r0 + r, kg = k0 + k;
+            if (rg >= R) return zero;
+            const float *p = X + rg * Kd + kg;
+            if constexpr (V) {
+                return kg < Kd ? ld4(p) : zero;  // Kd % 4 == 0: the quad is all in or all out
+            } else {
+                return make_float4(kg < Kd ? p[0] : 0.f, kg + 1 < Kd ? p[1] : 0.f, kg + 2 < Kd ? p[2] : 0.f,
+                                   kg + 3 < Kd ? p[3] : 0.f);
+            }
+        } else {
+            const size_t rg = r0 + r, kg = k0 + k;
+            if (kg >= Kd) return zero;
+            const float *p = X + kg * R + rg;
+            if constexpr (V) {
+                return rg < R ? ld4(p) : zero;  // R % 4 == 0
+            } else {
+                return make_float4(rg < R ? p[0] : 0.f, rg + 1 < R ? p[1] : 0.f, rg + 2 < R ? p[2] : 0.f,
+                                   rg + 3 < R ? p[3] : 0.f);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float (*Xs)[KPT], float4 v) const {
+        if constexpr (KC) {
+            *reinterpret_cast<float4 *>(&Xs[r][k]) = v;
+        } else {
+            Xs[r + 0][k] = v.x;
+            Xs[r + 1][k] = v.y;
+            Xs[r + 2][k] = v.z;
+            Xs[r + 3][k] = v.w;
+        }
+    }
+};
 
-    float *my = part + (static_cast<size_t>(tile) * splits + split) * (BM * BN);
-#pragma unroll
-    for (int i = 0; i < WI; ++i)
-#pragma unroll
-        for (int j = 0; j < WJ; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) st_dev(&my[out_row(i, r) * BN + out_col(j)], acc[i][j][r]);
-    if (!last_block_ticket(ctr(counters, tile), splits, &flag)) return;
-    // Sum the splits in split order; each round issues this lane's 64 loads together.
-    const float *tp = part + static_cast<size_t>(tile) * splits * (BM * BN);
+template <bool TA, bool TB, bool VA, bool VB, int BKT, bool XCDMAP = true>
+__global__ __launch_bounds__(kGemmThreads) void k_gemm_kc(const float *__restrict__ A, const float *__restrict__ B,
+                                                          float *__restrict__ C, size_t M, size_t N, size_t K,
+                                                          unsigned tiles_n, unsigned splits, size_t kper,
+                                                          Epilogue epi, float *__restrict__ part,
+                                                          unsigned *__restrict__ counters) {
+    constexpr int KPT = BKT + 4;
+    constexpr int SL = BM * BKT / 4 / kGemmThreads;  // staged quads per thread per operand
+    __shared__ float As[2][BM][KPT];
+    __shared__ float Bs[2][BN][KPT];
+    __shared__ int flag;
+    constexpr bool KCA = !TA, KCB = TB;
+
+    const unsigned wg = XCDMAP ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x;
+    const unsigned tile = wg / splits;
+    const unsigned split = wg - tile * splits;
+    const size_t m0 = static_cast<size_t>(tile / tiles_n) * BM;
+    const size_t n0 = static_cast<size_t>(tile % tiles_n) * BN;
+    const size_t kbeg = static_cast<size_t>(split) * kper;
+    const size_t kend = kbeg + kper < K ? kbeg + kper : K;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int wm = wave >> 2, wn = wave & 3;
+    const int l32 = lane & 31, lhi = lane >> 5;
+
+    floatx16 acc[WI][WJ];
 #pragma unroll
     for (int i = 0; i < WI; ++i)
 #pragma unroll
         for (int j = 0; j < WJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    for (unsigned s = 0; s < splits; ++s) {
-        float v[WI][WJ][16];
+
+    Stage<KCA, BKT> sa[SL];
+    Stage<KCB, BKT> sb[SL];
 #pragma unroll
-        for (int i = 0; i < WI; ++i)
-#pragma unroll
-            for (int j = 0; j < WJ; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) v[i][j][r] = ld_dev(&tp[s * (BM * BN) + out_row(i, r) * BN + out_col(j)]);
-#pragma unroll
-        for (int i = 0; i < WI; ++i)
-#pragma unroll
-            for (int j = 0; j < WJ; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + v[i][j][r];
+    for (int s = 0; s < SL; ++s) {
+        sa[s].init(tid + s * kGemmThreads);
+        sb[s].init(tid + s * kGemmThreads);
     }
+    float4 ra[SL], rb[SL];
+    int buf = 0;
+    if (kbeg < kend) {
 #pragma unroll
-    for (int i = 0; i < WI; ++i)
+        for (int s = 0; s < SL; ++s) {
+            ra[s] = sa[s].template load<VA>(A, m0, kbeg, M, K);
+            rb[s] = sb[s].template load<VB>(B, n0, kbeg, N, K);
+        }
+#pragma unroll
+        for (int s = 0; s < SL; ++s) {
+            sa[s].store(As[0], ra[s]);
+            sb[s].store(Bs[0], rb[s]);
+        }
+    }
+    __syncthreads();
+
+    for (size_t k0 = kbeg; k0 < kend; k0 += BKT) {
+        const bool more = k0 + BKT < kend;
+        if (more) {
+#pragma unroll
+            for (int s = 0; s < SL; ++s) {
+                ra[s] = sa[s].template load<VA>(A, m0, k0 + BKT, M, K);
+                rb[s] = sb[s].template load<VB>(B, n0, k0 + BKT, N, K);
+            }
+        }
+        // Blocks of 8 k: one b128 per fragment, the next block's reads in
+        // flight while this block's 4*WI*WJ MFMAs issue.
+        float4 fa[WI], fb[WJ];
+#pragma unroll
+        for (int i = 0; i < WI; ++i)
+            fa[i] = *reinterpret_cast<const float4 *>(&As[buf][wm * 64 + i * 32 + l32][4 * lhi]);
 #pragma unroll
         for (int j = 0; j < WJ; ++j)
+            fb[j] = *reinterpret_cast<const float4 *>(&Bs[buf][wn * 32 + j * 32 + l32][4 * lhi]);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const size_t row = m0 + out_row(i, r), col = n0 + out_col(j);
-                if (row < M && col < N) store_epi(epi, C, row, col, N, acc[i][j][r]);
+        for (int kb = 0; kb < BKT / 8; ++kb) {
+            float4 na[WI], nb[WJ];
+            if (kb + 1 < BKT / 8) {
+#pragma unroll
+                for (int i = 0; i < WI; ++i)
+                    na[i] = *reinterpret_cast<const float4 *>(&As[buf][wm * 64 + i * 32 + l32][8 * (kb + 1) + 4 * lhi]);
+#pragma unroll
+                for (int j = 0; j < WJ; ++j)
+                    nb[j] = *reinterpret_cast<const float4 *>(&Bs[buf][wn * 32 + j * 32 + l32][8 * (kb + 1) + 4 * lhi]);
             }
+#pragma unroll
+            for (int i = 0; i < WI; ++i)
+#pragma unroll
+                for (int j = 0; j < WJ; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i].x, fb[j].x, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i].y, fb[j].y, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i].z, fb[j].z, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i].w, fb[j].w, acc[i][j], 0, 0, 0);
+                }
+            if (kb + 1 < BKT / 8) {
+#pragma unroll
+                for (int i = 0; i < WI; ++i) fa[i] = na[i];
+#pragma unroll
+                for (int j = 0; j < WJ; ++j) fb[j] = nb[j];
+            }
+        }
+        // Scheduling groups: reads of block 0, then (reads of block b+1, MFMAs of block b).
+        __builtin_amdgcn_sched_group_barrier(0x100, WI + WJ, 0);
+#pragma unroll
+        for (int kb = 0; kb < BKT / 8; ++kb) {
+            if (kb + 1 < BKT / 8) __builtin_amdgcn_sched_group_barrier(0x100, WI + WJ, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * WI * WJ, 0);
+        }
+        if (more) {
+#pragma unroll
+            for (int s = 0; s < SL; ++s) {
+                sa[s].store(As[buf ^ 1], ra[s]);
+                sb[s].store(Bs[buf ^ 1], rb[s]);
+            }
+        }
+        __syncthreads();
+        buf ^= 1;
+    }
+    gemm_epilogue<WI, WJ>(acc, C, M, N, m0, n0, tile, split, splits, wm, wn, lhi, l32, epi, part, counters, &flag);
+}
+
+// ------------------------------------------------ four waves of 64x64
+//
+// The k-contiguous tiles of k_gemm_kc, but a 256-thread workgroup of four
+// waves (one per SIMD), each owning 64x64 of C = 2x2 MFMA tiles of 32x32
+// (64 accumulator registers).  Two b128 reads of A and two of B feed 16
+// MFMAs.  The next k step's tile, already in registers, is written to the
+// other LDS buffer three quarters of the way through this step's MFMAs, so
+// only the barrier separates two steps.
+constexpr int kW4Threads = 256;
+
+template <bool TA, bool TB, bool VA, bool VB, int BKT, bool XCDMAP = true>
+__global__ __launch_bounds__(kW4Threads) void k_gemm_w4(const float *__restrict__ A, const float *__restrict__ B,
+                                                        float *__restrict__ C, size_t M, size_t N, size_t K,
+                                                        unsigned tiles_n, unsigned splits, size_t kper,
+                                                        Epilogue epi, float *__restrict__ part,
+                                                        unsigned *__restrict__ counters) {
+    constexpr int KPT = BKT + 4;
+    constexpr int SL = BM * BKT / 4 / kW4Threads;  // staged quads per thread per operand
+    constexpr int W4I = 2, W4J = 2;
+    constexpr int NB = BKT / 8;             // k blocks of 8 per step
+    constexpr int WAT = (3 * NB) / 4;       // LDS writes after this many blocks
+    __shared__ float As[2][BM][KPT];
+    __shared__ float Bs[2][BN][KPT];
+    __shared__ int flag;
+    constexpr bool KCA = !TA, KCB = TB;
+
+    const unsigned wg = XCDMAP ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x;
+    const unsigned tile = wg / splits;
+    const unsigned split = wg - tile * splits;
+    const size_t m0 = static_cast<size_t>(tile / tiles_n) * BM;
+    const size_t n0 = static_cast<size_t>(tile % tiles_n) * BN;
+    const size_t kbeg = static_cast<size_t>(split) * kper;
+    const size_t kend = kbeg + kper < K ? kbeg + kper : K;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l32 = lane & 31, lhi = lane >> 5;
+
+    floatx16 acc[W4I][W4J];
+#pragma unroll
+    for (int i = 0; i < W4I; ++i)
+#pragma unroll
+        for (int j = 0; j < W4J; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    Stage<KCA, BKT> sa[SL];
+    Stage<KCB, BKT> sb[SL];
+#pragma unroll
+    for (int s = 0; s < SL; ++s) {
+        sa[s].init(tid + s * kW4Threads);
+        sb[s].init(tid + s * kW4Threads);
+    }
+    float4 ra[SL], rb[SL];
+    int buf = 0;
+    if (kbeg < kend) {
+#pragma unroll
+        for (int s = 0; s < SL; ++s) {
+            ra[s] = sa[s].template load<VA>(A, m0, kbeg, M, K);
+            rb[s] = sb[s].template load<VB>(B, n0, kbeg, N, K);
+        }
+#pragma unroll
+        for (int s = 0; s < SL; ++s) {
+            sa[s].store(As[0], ra[s]);
+            sb[s].store(Bs[0], rb[s]);
+        }
+    }
+    __syncthreads();
+
+    for (size_t k0 = kbeg; k0 < kend; k0 += BKT) {
+        const bool more = k0 + BKT < kend;
+        if (more) {
+#pragma unroll
+            for (int s = 0; s < SL; ++s) {
+                ra[s] = sa[s].template load<VA>(A, m0, k0 + BKT, M, K);
+                rb[s] = sb[s].template load<VB>(B, n0, k0 + BKT, N, K);
+            }
+        }
+        float4 fa[W4I], fb[W4J];
+#pragma unroll
+        for (int i = 0; i < W4I; ++i)
+            fa[i] = *reinterpret_cast<const float4 *>(&As[buf][wm * 64 + i * 32 + l32][4 * lhi]);
+#pragma unroll
+        for (int j = 0; j < W4J; ++j)
+            fb[j] = *reinterpret_cast<const float4 *>(&Bs[buf][wn * 64 + j * 32 + l32][4 * lhi]);
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+            float4 na[W4I], nb[W4J];
+            if (kb + 1 < NB) {
+#pragma unroll
+                for (int i = 0; i < W4I; ++i)
+                    na[i] = *reinterpret_cast<const float4 *>(&As[buf][wm * 64 + i * 32 + l32][8 * (kb + 1) + 4 * lhi]);
+#pragma unroll
+                for (int j = 0; j < W4J; ++j)
+                    nb[j] = *reinterpret_cast<const float4 *>(&Bs[buf][wn * 64 + j * 32 + l32][8 * (kb + 1) + 4 * lhi]);
+            }
+#pragma unroll
+            for (int i = 0; i < W4I; ++i)
+#pragma unroll
+                for (int j = 0; j < W4J; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i].x, fb[j].x, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i].y, fb[j].y, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i].z, fb[j].z, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i].w, fb[j].w, acc[i][j], 0, 0, 0);
+                }
+            if (kb + 1 == WAT && more) {
+                // the other buffer was last read before the previous barrier
+#pragma unroll
+                for (int s = 0; s < SL; ++s) {
+                    sa[s].store(As[buf ^ 1], ra[s]);
+                    sb[s].store(Bs[buf ^ 1], rb[s]);
+                }
+            }
+            if (kb + 1 < NB) {
+#pragma unroll
+                for (int i = 0; i < W4I; ++i) fa[i] = na[i];
+#pragma unroll
+                for (int j = 0; j < W4J; ++j) fb[j] = nb[j];
+            }
+        }
+        // Scheduling groups: reads of block 0; then per block the next
+        // block's reads and this block's MFMAs, with the LDS writes of the
+        // next tile after block WAT-1.
+        __builtin_amdgcn_sched_group_barrier(0x100, W4I + W4J, 0);
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+            if (kb + 1 < NB) __builtin_amdgcn_sched_group_barrier(0x100, W4I + W4J, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * W4I * W4J, 0);
+            if (kb + 1 == WAT) __builtin_amdgcn_sched_group_barrier(0x200, SL * ((KCA ? 1 : 4) + (KCB ? 1 : 4)), 0);
+        }
+        __syncthreads();
+        buf ^= 1;
+    }
+    gemm_epilogue<W4I, W4J>(acc, C, M, N, m0, n0, tile, split, splits, wm, wn, lhi, l32, epi, part, counters, &flag);
 }
 
 // ------------------------------------------------ skinny products
@@ -506,13 +860,52 @@ __global__ __launch_bounds__(kThinNT) void k_gemm_thin_k(const float *__restrict
     }
 }
 
+// Kernel variant per launch.  -1 (the library's setting) chooses by shape;
+// a tuning program that compiles this file can pin one: 0 k-major, 1/2
+// k-contiguous with BK 32/64, 3/4 four-wave with BK 32/64, 5 k-contiguous
+// without the XCD renumbering, 6 k-major with it.
+int g_gemm_kc = -1;
+
+// Measured on gfx950 (TFLOP/s, best variant vs the others):
+//  * grids of >= 1024 workgroups (8192^3, 4096^3): four waves of 64x64, BK 32
+//    (125 / 115 against <= 116 / 113);
+//  * A^T B (the MLP's weight gradients, split K): k-major tiles with the XCD
+//    renumbering (97.5 and 77 against 87-89 and 70-75);
+//  * A B and A B^T at 256-tile grids: k-contiguous tiles, BK 32, with the
+//    renumbering (93 and 104 against 90 and 94 for the k-major kernel).
+inline int gemm_variant(bool ta, bool tb, unsigned wgs) {
+    if (g_gemm_kc >= 0) return g_gemm_kc;
+    if (wgs >= 1024) return 3;
+    if (ta && !tb) return 6;
+    return 1;
+}
+
 template <bool TA, bool TB>
 int launch_t(const float *A, const float *B, float *C, size_t M, size_t N, size_t K, bool va, bool vb,
              dim3 grid, unsigned tiles_n, unsigned splits, size_t kper, Epilogue epi, float *part,
-             unsigned *counters, hipStream_t s) {
+             unsigned *counters, hipStream_t s, int variant) {
 #define CXM_GEMM_LAUNCH(VA_, VB_)                                                                  \
-    hipLaunchKernelGGL((k_gemm<TA, TB, VA_, VB_>), grid, dim3(kGemmThreads), 0, s, A, B, C, M, N, K, tiles_n, \
-                       splits, kper, epi, part, counters)
+    if (variant == 5)                                                                              \
+        hipLaunchKernelGGL((k_gemm_kc<TA, TB, VA_, VB_, 32, false>), grid, dim3(kGemmThreads), 0, s, A, B, C, M, N, \
+                           K, tiles_n, splits, kper, epi, part, counters);                        \
+    else if (variant == 6)                                                                         \
+        hipLaunchKernelGGL((k_gemm<TA, TB, VA_, VB_, true>), grid, dim3(kGemmThreads), 0, s, A, B, C, M, N, K,     \
+                           tiles_n, splits, kper, epi, part, counters);                           \
+    else if (variant == 3)                                                                         \
+        hipLaunchKernelGGL((k_gemm_w4<TA, TB, VA_, VB_, 32>), grid, dim3(kW4Threads), 0, s, A, B, C, M, N, K, \
+                           tiles_n, splits, kper, epi, part, counters);                           \
+    else if (variant == 4)                                                                         \
+        hipLaunchKernelGGL((k_gemm_w4<TA, TB, VA_, VB_, 64>), grid, dim3(kW4Threads), 0, s, A, B, C, M, N, K, \
+                           tiles_n, splits, kper, epi, part, counters);                           \
+    else if (variant == 2)                                                                         \
+        hipLaunchKernelGGL((k_gemm_kc<TA, TB, VA_, VB_, 64>), grid, dim3(kGemmThreads), 0, s, A, B, C, M, N, K, \
+                           tiles_n, splits, kper, epi, part, counters);                           \
+    else if (variant == 1)                                                                         \
+        hipLaunchKernelGGL((k_gemm_kc<TA, TB, VA_, VB_, 32>), grid, dim3(kGemmThreads), 0, s, A, B, C, M, N, K, \
+                           tiles_n, splits, kper, epi, part, counters);                           \
+    else                                                                                           \
+        hipLaunchKernelGGL((k_gemm<TA, TB, VA_, VB_>), grid, dim3(kGemmThreads), 0, s, A, B, C, M, N, K, tiles_n, \
+                           splits, kper, epi, part, counters)
     if (va && vb) CXM_GEMM_LAUNCH(true, true);
     else if (va) CXM_GEMM_LAUNCH(true, false);
     else if (vb) CXM_GEMM_LAUNCH(false, true);
@@ -586,8 +979,11 @@ int gemm_ex(const float *A, const float *B, float *C, size_t M, size_t K, size_t
         if (splits > max_splits) splits = max_splits;
         if (splits < 1) splits = 1;
     }
+    // a split's k range is a whole number of the kernel's k steps
+    const int variant = gemm_variant(ta, tb, static_cast<unsigned>(tiles * splits));
+    const size_t kstep = (variant == 2 || variant == 4) ? 64 : BK;
     size_t kper = (K + splits - 1) / splits;
-    kper = (kper + BK - 1) / BK * BK;
+    kper = (kper + kstep - 1) / kstep * kstep;
     splits = (K + kper - 1) / kper;
     if (tiles * splits > 0x7fffffffu) return CXM_E_TOO_LARGE;
     float *part = nullptr;
@@ -605,10 +1001,10 @@ int gemm_ex(const float *A, const float *B, float *C, size_t M, size_t K, size_t
     const dim3 grid(static_cast<unsigned>(tiles * splits));
     hipStream_t s = reinterpret_cast<hipStream_t>(st);
     const unsigned tn = static_cast<unsigned>(tiles_n), sp = static_cast<unsigned>(splits);
-    if (!ta && !tb) return launch_t<false, false>(A, B, C, M, N, K, va, vb, grid, tn, sp, kper, epi, part, counters, s);
-    if (ta && !tb) return launch_t<true, false>(A, B, C, M, N, K, va, vb, grid, tn, sp, kper, epi, part, counters, s);
-    if (!ta && tb) return launch_t<false, true>(A, B, C, M, N, K, va, vb, grid, tn, sp, kper, epi, part, counters, s);
-    return launch_t<true, true>(A, B, C, M, N, K, va, vb, grid, tn, sp, kper, epi, part, counters, s);
+    if (!ta && !tb) return launch_t<false, false>(A, B, C, M, N, K, va, vb, grid, tn, sp, kper, epi, part, counters, s, variant);
+    if (ta && !tb) return launch_t<true, false>(A, B, C, M, N, K, va, vb, grid, tn, sp, kper, epi, part, counters, s, variant);
+    if (!ta && tb) return launch_t<false, true>(A, B, C, M, N, K, va, vb, grid, tn, sp, kper, epi, part, counters, s, variant);
+    return launch_t<true, true>(A, B, C, M, N, K, va, vb, grid, tn, sp, kper, epi, part, counters, s, variant);
 }
 
 }  // namespace cxm

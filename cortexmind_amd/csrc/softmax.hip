@@ -31,12 +31,12 @@ constexpr float kLowest = -FLT_MAX;
 
 // ------------------------------------------------- wave per row, registers
 
-// NV float4 per lane: cols <= 256 * NV.  4 rows per 256-thread workgroup.
-template <int NV, bool LOG>
-__global__ __launch_bounds__(kBlock) void k_sm_fwd_wave(const float *__restrict__ x,
-                                                        float *__restrict__ y, size_t rows,
-                                                        size_t cols) {
-    const size_t row = static_cast<size_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
+// NV float4 per lane: cols <= 256 * NV.  WPB rows (one per wave) per workgroup.
+template <int NV, bool LOG, int WPB = kWavesPerBlock>
+__global__ __launch_bounds__(WPB * kWave) void k_sm_fwd_wave(const float *__restrict__ x,
+                                                             float *__restrict__ y, size_t rows,
+                                                             size_t cols) {
+    const size_t row = static_cast<size_t>(blockIdx.x) * WPB + threadIdx.x / kWave;
     if (row >= rows) return;  // whole waves leave together
     const int lane = threadIdx.x & (kWave - 1);
     const float *__restrict__ xr = x + row * cols;
@@ -84,12 +84,12 @@ __global__ __launch_bounds__(kBlock) void k_sm_fwd_wave(const float *__restrict_
 
 // Backward from the saved output: softmax dx = y*(dy - sum(dy*y)),
 // log-softmax dx = dy - exp(y)*sum(dy).
-template <int NV, bool LOG>
-__global__ __launch_bounds__(kBlock) void k_sm_bwd_wave(const float *__restrict__ y,
-                                                        const float *__restrict__ dy,
-                                                        float *__restrict__ dx, size_t rows,
-                                                        size_t cols) {
-    const size_t row = static_cast<size_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
+template <int NV, bool LOG, int WPB = kWavesPerBlock>
+__global__ __launch_bounds__(WPB * kWave) void k_sm_bwd_wave(const float *__restrict__ y,
+                                                             const float *__restrict__ dy,
+                                                             float *__restrict__ dx, size_t rows,
+                                                             size_t cols) {
+    const size_t row = static_cast<size_t>(blockIdx.x) * WPB + threadIdx.x / kWave;
     if (row >= rows) return;
     const int lane = threadIdx.x & (kWave - 1);
     const size_t off = row * cols;
@@ -421,27 +421,32 @@ inline hipStream_t hs(cxm_stream_t s) { return reinterpret_cast<hipStream_t>(s);
 
 constexpr size_t kWaveRowMax = 256 * 16;  // wave-per-row kernel holds up to 4096 columns
 
+// Two rows (waves) per workgroup: measured on [512, 1024] as 3.35 us per
+// launch against 3.5-3.8 us with four or eight rows per workgroup (more
+// workgroups spread the rows over more CUs).
+constexpr int kSmWpb = 2;
+
 template <bool LOG>
 int sm_fwd_wave(const float *x, float *y, size_t rows, size_t cols, hipStream_t s) {
-    const dim3 grid(ceil_div(rows, kWavesPerBlock));
+    const dim3 grid(ceil_div(rows, kSmWpb)), block(kSmWpb * kWave);
     const size_t nv = (cols + 255) / 256;
-    if (nv <= 1) hipLaunchKernelGGL((k_sm_fwd_wave<1, LOG>), grid, dim3(kBlock), 0, s, x, y, rows, cols);
-    else if (nv <= 2) hipLaunchKernelGGL((k_sm_fwd_wave<2, LOG>), grid, dim3(kBlock), 0, s, x, y, rows, cols);
-    else if (nv <= 4) hipLaunchKernelGGL((k_sm_fwd_wave<4, LOG>), grid, dim3(kBlock), 0, s, x, y, rows, cols);
-    else if (nv <= 8) hipLaunchKernelGGL((k_sm_fwd_wave<8, LOG>), grid, dim3(kBlock), 0, s, x, y, rows, cols);
-    else hipLaunchKernelGGL((k_sm_fwd_wave<16, LOG>), grid, dim3(kBlock), 0, s, x, y, rows, cols);
+    if (nv <= 1) hipLaunchKernelGGL((k_sm_fwd_wave<1, LOG, kSmWpb>), grid, block, 0, s, x, y, rows, cols);
+    else if (nv <= 2) hipLaunchKernelGGL((k_sm_fwd_wave<2, LOG, kSmWpb>), grid, block, 0, s, x, y, rows, cols);
+    else if (nv <= 4) hipLaunchKernelGGL((k_sm_fwd_wave<4, LOG, kSmWpb>), grid, block, 0, s, x, y, rows, cols);
+    else if (nv <= 8) hipLaunchKernelGGL((k_sm_fwd_wave<8, LOG, kSmWpb>), grid, block, 0, s, x, y, rows, cols);
+    else hipLaunchKernelGGL((k_sm_fwd_wave<16, LOG, kSmWpb>), grid, block, 0, s, x, y, rows, cols);
     return launch_status();
 }
 
 template <bool LOG>
 int sm_bwd_wave(const float *y, const float *dy, float *dx, size_t rows, size_t cols, hipStream_t s) {
-    const dim3 grid(ceil_div(rows, kWavesPerBlock));
+    const dim3 grid(ceil_div(rows, kSmWpb)), block(kSmWpb * kWave);
     const size_t nv = (cols + 255) / 256;
-    if (nv <= 1) hipLaunchKernelGGL((k_sm_bwd_wave<1, LOG>), grid, dim3(kBlock), 0, s, y, dy, dx, rows, cols);
-    else if (nv <= 2) hipLaunchKernelGGL((k_sm_bwd_wave<2, LOG>), grid, dim3(kBlock), 0, s, y, dy, dx, rows, cols);
-    else if (nv <= 4) hipLaunchKernelGGL((k_sm_bwd_wave<4, LOG>), grid, dim3(kBlock), 0, s, y, dy, dx, rows, cols);
-    else if (nv <= 8) hipLaunchKernelGGL((k_sm_bwd_wave<8, LOG>), grid, dim3(kBlock), 0, s, y, dy, dx, rows, cols);
-    else hipLaunchKernelGGL((k_sm_bwd_wave<16, LOG>), grid, dim3(kBlock), 0, s, y, dy, dx, rows, cols);
+    if (nv <= 1) hipLaunchKernelGGL((k_sm_bwd_wave<1, LOG, kSmWpb>), grid, block, 0, s, y, dy, dx, rows, cols);
+    else if (nv <= 2) hipLaunchKernelGGL((k_sm_bwd_wave<2, LOG, kSmWpb>), grid, block, 0, s, y, dy, dx, rows, cols);
+    else if (nv <= 4) hipLaunchKernelGGL((k_sm_bwd_wave<4, LOG, kSmWpb>), grid, block, 0, s, y, dy, dx, rows, cols);
+    else if (nv <= 8) hipLaunchKernelGGL((k_sm_bwd_wave<8, LOG, kSmWpb>), grid, block, 0, s, y, dy, dx, rows, cols);
+    else hipLaunchKernelGGL((k_sm_bwd_wave<16, LOG, kSmWpb>), grid, block, 0, s, y, dy, dx, rows, cols);
     return launch_status();
 }
 

@@ -70,6 +70,20 @@ def test_gemm_full_size_float64(hip, m, k, n):
     assert np.all(np.abs(got - ref) <= bound(a, b))
 
 
+@pytest.mark.parametrize("m,k,n", [(4096, 256, 4096), (4100, 300, 4095)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_gemm_large_grid_float64(hip, m, k, n, ta, tb):
+    """Grids of >= 1024 tiles take the four-wave kernel; ragged edges included."""
+    g = SplitMix64(m + 3 * k + 7 * n + 11 * ta + 13 * tb)
+    a = g.normal((m, k))
+    b = g.normal((k, n))
+    bias = g.normal((n,), 0.0, 0.5)
+    got = run(a, b, ta, tb, bias=bias, act=ACT_RELU)
+    z = a.astype(np.float64) @ b.astype(np.float64) + bias.astype(np.float64)
+    ref = np.maximum(z, 0.0)
+    assert np.all(np.abs(got - ref) <= bound(a, b) + 1e-6 * np.abs(bias)[None, :])
+
+
 def test_epilogue_bias_relu_gate(hip, orc):
     g = SplitMix64(17)
     a, b = g.normal((200, 96)), g.normal((96, 72))
