@@ -31,6 +31,13 @@ _SZ = ctypes.c_size_t
 _I = ctypes.c_int
 _F = ctypes.c_float
 
+class PoolStats(ctypes.Structure):
+    """cxm_pool_stats_t."""
+    _fields_ = [("bytes_in_use", ctypes.c_size_t), ("bytes_cached", ctypes.c_size_t),
+                ("peak_in_use", ctypes.c_size_t), ("allocs", ctypes.c_uint64), ("hits", ctypes.c_uint64),
+                ("frees", ctypes.c_uint64), ("device_allocs", ctypes.c_uint64)]
+
+
 # name -> argtypes (every function returns int status)
 SIGNATURES = {
     "cxm_device_count": [ctypes.POINTER(_I)],
@@ -52,6 +59,11 @@ SIGNATURES = {
     "cxm_event_elapsed_ms": [ctypes.POINTER(_F), _P, _P],
     "cxm_event_destroy": [_P],
     "cxm_release_workspaces": [],
+    "cxm_act_bwd_f32": [_P, _P, _P, _SZ, _I, _P],
+    "cxm_pool_alloc": [ctypes.POINTER(_P), _SZ, _P],
+    "cxm_pool_free": [_P],
+    "cxm_pool_release": [],
+    "cxm_pool_stats": [_P],
     "cxm_reduce_sum_flat_f32": [_P, _P, _SZ, _P],
     "cxm_reduce_mean_flat_f32": [_P, _P, _SZ, _P],
     "cxm_reduce_max_flat_f32": [_P, _P, _SZ, _P],

@@ -45,6 +45,9 @@ struct Workspace {
 };
 int get_workspace(cxm_stream_t s, size_t counters, size_t scratch_bytes, Workspace *ws);
 
+// Returns the caching pool's blocks of a stream to the device (pool.hip).
+int pool_drop_stream(cxm_stream_t s);
+
 __host__ __device__ inline unsigned *ctr(unsigned *base, size_t i) { return base + i * kCtr; }
 
 // Epilogue of the GEMM (gemm.hip), applied to each finished sum

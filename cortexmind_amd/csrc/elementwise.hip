@@ -171,6 +171,11 @@ struct AffineF {
         return act4<ACT>(t);
     }
 };
+// dx = dy * act'(y), the derivative factor from the saved output
+template <int ACT>
+struct ActBwdF {
+    __device__ float operator()(float y, float g) const { return g * dact<ACT>(y); }
+};
 // w - g*lr, two roundings
 struct SgdF {
     float lr;
@@ -344,6 +349,17 @@ __global__ __launch_bounds__(NW * kWave) void k_affine_bwd(const float *__restri
 // ------------------------------------------------------------------ sgd
 
 // w = w - g*lr, two roundings (matrix_t::sub of ScalarOp::mul).
+__global__ __launch_bounds__(kBlock) void k_act_bwd_scalar(const float *y, const float *dy, float *dx, size_t n,
+                                                            int act) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        const float yy = y[i];
+        const float d = act == CXM_ACT_RELU ? dact<CXM_ACT_RELU>(yy)
+                                            : (act == CXM_ACT_SIGMOID ? dact<CXM_ACT_SIGMOID>(yy) : dact<CXM_ACT_TANH>(yy));
+        dx[i] = dy[i] * d;
+    }
+}
+
 __global__ __launch_bounds__(kBlock) void k_sgd_scalar(float *w, const float *g, float lr, size_t n) {
     const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
     for (size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
@@ -576,6 +592,32 @@ int cxm_affine_act_bwd_f32(const float *x, const float *scale, const float *y, c
             return affine_bwd_t<CXM_ACT_TANH>(x, scale, y, dy, dx, dscale, dbias, m, n, s);
         default: return CXM_E_INVALID;
     }
+}
+
+int cxm_act_bwd_f32(const float *y, const float *dy, float *dx, size_t n, int act, cxm_stream_t s) {
+    if (!y || !dy || !dx || act < CXM_ACT_RELU || act > CXM_ACT_TANH) return CXM_E_INVALID;
+    if (n == 0) return CXM_OK;
+    if (!(aligned16(y) && aligned16(dy) && aligned16(dx))) {
+        hipLaunchKernelGGL(k_act_bwd_scalar, dim3(stream_grid((n + 3) / 4)), dim3(kBlock), 0, hs(s), y, dy, dx, n,
+                           act);
+        return launch_status();
+    }
+    const unsigned g = map4_grid(n);
+    if (!g) return CXM_E_TOO_LARGE;
+    switch (act) {
+        case CXM_ACT_RELU:
+            hipLaunchKernelGGL(k_zip4<ActBwdF<CXM_ACT_RELU>>, dim3(g), dim3(kBlock), 0, hs(s), ActBwdF<CXM_ACT_RELU>{},
+                               y, dy, dx, n);
+            break;
+        case CXM_ACT_SIGMOID:
+            hipLaunchKernelGGL(k_zip4<ActBwdF<CXM_ACT_SIGMOID>>, dim3(g), dim3(kBlock), 0, hs(s),
+                               ActBwdF<CXM_ACT_SIGMOID>{}, y, dy, dx, n);
+            break;
+        default:
+            hipLaunchKernelGGL(k_zip4<ActBwdF<CXM_ACT_TANH>>, dim3(g), dim3(kBlock), 0, hs(s), ActBwdF<CXM_ACT_TANH>{},
+                               y, dy, dx, n);
+    }
+    return launch_status();
 }
 
 int cxm_sgd_f32(float *w, const float *g, float lr, size_t n, cxm_stream_t s) {

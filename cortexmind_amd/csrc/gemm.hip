@@ -329,7 +329,9 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(const float *__restrict__
 // block, lanes 0-31 supply k = kb + j and lanes 32-63 k = kb + 4 + j, so the
 // four MFMAs still cover each k of the block exactly once.  With the stride
 // of 36 floats, the 16-lane phases of a b128 read hit 16 distinct 4-bank
-// groups.
+// groups.  The next k step's tile, already in registers, is written to the
+// other LDS buffer three quarters of the way through this step's MFMAs, so
+// only the barrier separates two steps.
 
 // Staging of one operand tile (128 rows r = m or n, BK = 32 k) through
 // registers into the k-contiguous LDS tile Xs[r][k].
@@ -399,6 +401,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_kc(const float *__restric
                                                           unsigned *__restrict__ counters) {
     constexpr int KPT = BKT + 4;
     constexpr int SL = BM * BKT / 4 / kGemmThreads;  // staged quads per thread per operand
+    constexpr int WAT = (3 * (BKT / 8)) / 4;        // LDS writes of the next tile after this many k blocks
     __shared__ float As[2][BM][KPT];
     __shared__ float Bs[2][BN][KPT];
     __shared__ int flag;
@@ -487,6 +490,14 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_kc(const float *__restric
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i].z, fb[j].z, acc[i][j], 0, 0, 0);
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i].w, fb[j].w, acc[i][j], 0, 0, 0);
                 }
+            if (kb + 1 == WAT && more) {
+                // the other buffer was last read before the previous barrier
+#pragma unroll
+                for (int s = 0; s < SL; ++s) {
+                    sa[s].store(As[buf ^ 1], ra[s]);
+                    sb[s].store(Bs[buf ^ 1], rb[s]);
+                }
+            }
             if (kb + 1 < BKT / 8) {
 #pragma unroll
                 for (int i = 0; i < WI; ++i) fa[i] = na[i];
@@ -500,13 +511,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_kc(const float *__restric
         for (int kb = 0; kb < BKT / 8; ++kb) {
             if (kb + 1 < BKT / 8) __builtin_amdgcn_sched_group_barrier(0x100, WI + WJ, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 4 * WI * WJ, 0);
-        }
-        if (more) {
-#pragma unroll
-            for (int s = 0; s < SL; ++s) {
-                sa[s].store(As[buf ^ 1], ra[s]);
-                sb[s].store(Bs[buf ^ 1], rb[s]);
-            }
+            if (kb + 1 == WAT) __builtin_amdgcn_sched_group_barrier(0x200, SL * ((KCA ? 1 : 4) + (KCB ? 1 : 4)), 0);
         }
         __syncthreads();
         buf ^= 1;

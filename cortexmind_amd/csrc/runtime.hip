@@ -172,6 +172,9 @@ int cxm_stream_sync(cxm_stream_t s) { return st(hipStreamSynchronize(reinterpret
 
 int cxm_stream_destroy(cxm_stream_t s) {
     if (!s) return CXM_E_INVALID;
+    // cached pool blocks of this stream go back to the device: a new stream
+    // may reuse the handle value
+    (void)cxm::pool_drop_stream(s);
     {
         // Drop this stream's workspaces before the handle can be reused.
         std::lock_guard<std::mutex> lk(g_ws_mu);

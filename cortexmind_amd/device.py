@@ -69,16 +69,22 @@ class Event:
 
 
 class DeviceArray:
-    """A contiguous device buffer with a numpy dtype and shape."""
+    """A contiguous device buffer with a numpy dtype and shape.  With
+    pool=True the memory comes from the library's stream-ordered caching
+    allocator (cxm_pool_alloc on `stream`) instead of a direct allocation."""
 
-    def __init__(self, shape, dtype=np.float32):
+    def __init__(self, shape, dtype=np.float32, pool: bool = False, stream: "Stream | None" = None):
         self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
         self.dtype = np.dtype(dtype)
         self.size = int(np.prod(self.shape)) if self.shape else 1
         self.nbytes = self.size * self.dtype.itemsize
         self._ptr = ctypes.c_void_p(None)
+        self._pool = bool(pool)
         if self.nbytes:
-            call("cxm_dev_malloc", ctypes.byref(self._ptr), self.nbytes)
+            if self._pool:
+                call("cxm_pool_alloc", ctypes.byref(self._ptr), self.nbytes, stream.handle if stream else None)
+            else:
+                call("cxm_dev_malloc", ctypes.byref(self._ptr), self.nbytes)
 
     @property
     def ptr(self) -> int | None:
@@ -116,13 +122,13 @@ class DeviceArray:
 
     def free(self) -> None:
         if self._ptr.value:
-            call("cxm_dev_free", self._ptr)
+            call("cxm_pool_free" if self._pool else "cxm_dev_free", self._ptr)
             self._ptr = ctypes.c_void_p(None)
 
     def __del__(self):
         try:
             if self._ptr.value and not _exiting:
-                lib().cxm_dev_free(self._ptr)
+                (lib().cxm_pool_free if self._pool else lib().cxm_dev_free)(self._ptr)
                 self._ptr = ctypes.c_void_p(None)
         except Exception:
             pass
@@ -140,3 +146,16 @@ def device_info() -> dict:
     cus = ctypes.c_int(0)
     call("cxm_device_info", name, 256, ctypes.byref(cus), arch, 256)
     return {"name": name.value.decode(), "arch": arch.value.decode(), "cus": cus.value}
+
+
+def pool_stats() -> dict:
+    """The caching allocator's counters (cxm_pool_stats)."""
+    from ._lib import PoolStats
+
+    st = PoolStats()
+    call("cxm_pool_stats", ctypes.byref(st))
+    return {name: int(getattr(st, name)) for name, _ in PoolStats._fields_}
+
+
+def pool_release() -> None:
+    call("cxm_pool_release")

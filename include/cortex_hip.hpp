@@ -16,6 +16,10 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <utility>
+#include <vector>
 
 #include "cxm_hip.h"
 
@@ -190,6 +194,165 @@ struct activation {
     static void sigmoid(const float *Xx, float *Xz, std::size_t N) { check(cxm_unary_f32(Xx, Xz, N, CXM_ACT_SIGMOID, stream()), "sigmoid"); }
     static void tanh(const float *Xx, float *Xz, std::size_t N) { check(cxm_unary_f32(Xx, Xz, N, CXM_ACT_TANH, stream()), "tanh"); }
     static void exp(const float *Xx, float *Xz, std::size_t N) { check(cxm_unary_f32(Xx, Xz, N, CXM_ACT_EXP, stream()), "exp"); }
+};
+
+// ------------------------------------------------------------ storage
+
+// The reference's DeviceType (Memory/type.hpp:22-26) with the HIP device
+// this backend adds.
+enum class DeviceType : std::uint8_t { Unknown = 0, HOST = 1, CUDA = 2, HIP = 3 };
+
+// TensorStorage (Storage/storage.hpp:14-57) for the host and HIP devices:
+// an owning, move-only byte buffer.  HIP memory comes from the library's
+// stream-ordered caching pool (cxm_pool_alloc on hip::stream()), in place
+// of the reference's fixed 128 MiB ForgeChunk; host memory is 64-byte
+// aligned.  Unlike the reference's move assignment (Storage/operator.cpp:
+// 25-31, which frees the buffer it just took), moving transfers ownership.
+class Storage {
+public:
+    Storage() = default;
+    Storage(std::size_t bytes, DeviceType type) : bytes_(bytes), device_(type) {
+        if (bytes_ == 0) return;
+        if (type == DeviceType::HIP) {
+            void *p = nullptr;
+            check(cxm_pool_alloc(&p, bytes_, stream()), "Storage: device allocation");
+            data_ = static_cast<std::byte *>(p);
+        } else if (type == DeviceType::HOST) {
+            data_ = static_cast<std::byte *>(std::aligned_alloc(64, (bytes_ + 63) / 64 * 64));
+            if (!data_) check(CXM_E_INVALID, "Storage: host allocation");
+        } else {
+            check(CXM_E_INVALID, "Storage: unsupported device");
+        }
+    }
+    // A copy of `bytes` of host memory at `data` on device `type`.
+    Storage(std::size_t bytes, const std::byte *data, DeviceType type) : Storage(bytes, type) {
+        if (!bytes_) return;
+        if (type == DeviceType::HIP) check(cxm_memcpy_h2d(data_, data, bytes_, stream()), "Storage: upload");
+        else std::memcpy(data_, data, bytes_);
+        if (type == DeviceType::HIP) check(cxm_stream_sync(stream()), "Storage: upload");
+    }
+    Storage(const Storage &) = delete;
+    Storage &operator=(const Storage &) = delete;
+    Storage(Storage &&o) noexcept { swap(o); }
+    Storage &operator=(Storage &&o) noexcept {
+        if (this != &o) {
+            Storage t(std::move(o));
+            swap(t);
+        }
+        return *this;
+    }
+    ~Storage() { reset(); }
+
+    template <class T>
+    T *as() { return reinterpret_cast<T *>(data_); }
+    template <class T>
+    const T *as() const { return reinterpret_cast<const T *>(data_); }
+    std::byte *raw() noexcept { return data_; }
+    const std::byte *raw() const noexcept { return data_; }
+    std::size_t bytes() const noexcept { return bytes_; }
+    bool isEmpty() const noexcept { return bytes_ == 0; }
+    bool isValid() const noexcept { return data_ != nullptr || bytes_ == 0; }
+    DeviceType device() const noexcept { return device_; }
+
+    // A copy on the same device (TensorStorage::clone).
+    Storage clone() const { return copy_to(device_); }
+    // A copy on `type` (the data movement of Tensor::to, Tensor/tensor.cpp:151-171).
+    Storage copy_to(DeviceType type) const {
+        Storage out(bytes_, type);
+        if (!bytes_) return out;
+        if (device_ == DeviceType::HIP && type == DeviceType::HIP)
+            check(cxm_memcpy_d2d(out.data_, data_, bytes_, stream()), "Storage: copy");
+        else if (device_ == DeviceType::HIP)
+            check(cxm_memcpy_d2h(out.data_, data_, bytes_, stream()), "Storage: download");
+        else if (type == DeviceType::HIP) {
+            check(cxm_memcpy_h2d(out.data_, data_, bytes_, stream()), "Storage: upload");
+            check(cxm_stream_sync(stream()), "Storage: upload");
+        } else
+            std::memcpy(out.data_, data_, bytes_);
+        return out;
+    }
+
+private:
+    void swap(Storage &o) noexcept {
+        std::swap(data_, o.data_);
+        std::swap(bytes_, o.bytes_);
+        std::swap(device_, o.device_);
+    }
+    void reset() noexcept {
+        if (data_) {
+            if (device_ == DeviceType::HIP) (void)cxm_pool_free(data_);
+            else std::free(data_);
+        }
+        data_ = nullptr;
+        bytes_ = 0;
+    }
+    std::byte *data_ = nullptr;
+    std::size_t bytes_ = 0;
+    DeviceType device_ = DeviceType::Unknown;
+};
+
+// A dense row-major fp32 tensor on the host or the HIP device: the part of
+// the reference's Tensor (Tensor/tensor.hpp) the operators and the autograd
+// flows need -- shape, storage, device, to(), grad, the producing flow.
+struct GradientFlow;
+class Tensor {
+public:
+    Tensor() = default;
+    Tensor(std::vector<std::int64_t> shape, DeviceType d = DeviceType::HIP, bool requires_grad = false)
+        : shape_(std::move(shape)), requires_grad_(requires_grad) {
+        storage_ = std::make_shared<Storage>(len() * sizeof(float), d);
+    }
+    // A HIP tensor holding a copy of host data.
+    static Tensor from_host(std::vector<std::int64_t> shape, const float *data, bool requires_grad = false) {
+        Tensor t;
+        t.shape_ = std::move(shape);
+        t.requires_grad_ = requires_grad;
+        t.storage_ = std::make_shared<Storage>(t.len() * sizeof(float), reinterpret_cast<const std::byte *>(data),
+                                               DeviceType::HIP);
+        return t;
+    }
+
+    std::size_t len() const noexcept {
+        std::size_t n = 1;
+        for (auto d : shape_) n *= static_cast<std::size_t>(d);
+        return n;
+    }
+    std::size_t ndim() const noexcept { return shape_.size(); }
+    const std::vector<std::int64_t> &shape() const noexcept { return shape_; }
+    std::int64_t dim(std::size_t i) const { return shape_.at(i); }
+    DeviceType device() const noexcept { return storage_ ? storage_->device() : DeviceType::Unknown; }
+    bool empty() const noexcept { return !storage_ || storage_->isEmpty(); }
+    float *data() { return storage_->as<float>(); }
+    const float *data() const { return storage_->as<float>(); }
+
+    // Tensor::to (Tensor/tensor.cpp:151-171): moves the data to `type`.
+    Tensor &to(DeviceType type) {
+        if (device() != type) storage_ = std::make_shared<Storage>(storage_->copy_to(type));
+        return *this;
+    }
+    std::vector<float> host() const {
+        std::vector<float> out(len());
+        if (device() == DeviceType::HIP)
+            check(cxm_memcpy_d2h(out.data(), data(), len() * sizeof(float), stream()), "Tensor: download");
+        else
+            std::memcpy(out.data(), data(), len() * sizeof(float));
+        return out;
+    }
+
+    bool isRequired() const noexcept { return requires_grad_; }
+    bool has_grad() const noexcept { return grad_ != nullptr; }
+    Tensor &grad() { return *grad_; }
+    std::shared_ptr<Tensor> &grad_ptr() { return grad_; }
+    std::shared_ptr<GradientFlow> &flow() { return flow_; }
+    // Same tensor (shared storage, gradient and flow), as a handle.
+    std::shared_ptr<Storage> storage() const { return storage_; }
+
+private:
+    std::vector<std::int64_t> shape_;
+    std::shared_ptr<Storage> storage_;
+    std::shared_ptr<Tensor> grad_;
+    std::shared_ptr<GradientFlow> flow_;
+    bool requires_grad_ = false;
 };
 
 }  // namespace cortex::_fw::hip

@@ -102,6 +102,32 @@ int cxm_event_destroy(cxm_event_t e);
 /* Frees every workspace the library holds (waits for their streams first). */
 int cxm_release_workspaces(void);
 
+/* Stream-ordered caching allocator: the replacement for ForgeChunk
+ * (Memory/forge.cuh:30-90, forge.cu:13-122), the device branch of
+ * TensorStorage (Storage/storage.cpp:20-35).  Requests round up to a size
+ * class (powers of two from 512 B to 1 MiB, then multiples of 2 MiB).  A
+ * block belongs to the stream it was allocated on: freeing it returns it to
+ * that stream's cache, and only later allocations on the same stream reuse
+ * it, so the stream order makes reuse safe without host synchronisation.
+ * A block used on another stream needs the caller's synchronisation before
+ * it is freed.  When the device is out of memory the cache is returned to
+ * the device (after a device sync) and the allocation retried once.
+ * cxm_pool_free of a pointer the pool did not return is CXM_E_INVALID. */
+typedef struct cxm_pool_stats_t {
+    size_t bytes_in_use;   /* size classes of live blocks */
+    size_t bytes_cached;   /* size classes of freed blocks held for reuse */
+    size_t peak_in_use;
+    uint64_t allocs;       /* successful allocations */
+    uint64_t hits;         /* of which served from the cache */
+    uint64_t frees;
+    uint64_t device_allocs;  /* allocations that called hipMalloc */
+} cxm_pool_stats_t;
+int cxm_pool_alloc(void **ptr, size_t bytes, cxm_stream_t s);
+int cxm_pool_free(void *ptr);
+/* Returns all cached blocks to the device (waits for the device first). */
+int cxm_pool_release(void);
+int cxm_pool_stats(cxm_pool_stats_t *stats);
+
 /* ------------------------------------------------------------ reductions
  * avx2::reduce (Engine/AVX2/reduce.hpp:49-296, reduce.cpp:17-84,204-251,
  * 439-528).  The flat form reduces N elements to z[0]; the axis form treats
@@ -262,6 +288,12 @@ int cxm_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t k, s
  * dlogits = (softmax(logits) - onehot) / b.  No reference counterpart. */
 int cxm_softmax_xent_f32(const float *logits, const int32_t *labels, float *loss, float *dlogits,
                          size_t b, size_t c, cxm_stream_t s);
+/* dx = dy * act'(y) from the saved output y, act in RELU, SIGMOID, TANH:
+ * relu' = (y > 0 ? 1 : 0), sigmoid' = y*(1-y), tanh' = 1 - y*y, each factor
+ * rounded, then one product.  dx may alias dy.  No reference counterpart:
+ * the backward of avx2::relu/sigmoid/tanh (functions.hpp:372-411) that a
+ * concrete GradientFlow would run. */
+int cxm_act_bwd_f32(const float *y, const float *dy, float *dx, size_t n, int act, cxm_stream_t s);
 /* w -= lr * g, as matrix_t::sub(w, ScalarOp::mul(g, lr)): two roundings. */
 int cxm_sgd_f32(float *w, const float *g, float lr, size_t n, cxm_stream_t s);
 

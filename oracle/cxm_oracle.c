@@ -647,6 +647,13 @@ static inline float act_grad(int act, float y) {
     }
 }
 
+/* dx = dy * act'(y): the backward of relu/sigmoid/tanh from the saved
+ * output, as a concrete GradientFlow would run it (matrix_t::mul(dY, G),
+ * matrix.cpp:35-43, with G = act_grad(Y)). */
+void orc_act_bwd(const float *y, const float *dy, float *dx, size_t n, int act) {
+    for (size_t i = 0; i < n; ++i) dx[i] = dy[i] * act_grad(act, y[i]);
+}
+
 /* Affine + activation forward: T = row::mul(X, scale) (broadcast.cpp:206-216),
  * row::add(T, bias) in place (broadcast.cpp:230-240), Y = act(T). */
 void orc_affine_act_fwd(const float *x, const float *scale, const float *bias, float *y,

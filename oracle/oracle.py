@@ -64,6 +64,7 @@ def lib() -> ctypes.CDLL:
             "orc_scalar": [_F, ctypes.c_float, _F, _SZ, ctypes.c_int],
             "orc_unary": [_F, _F, _SZ, ctypes.c_int],
             "orc_wise": [_F, _F, _SZ, ctypes.c_int],
+            "orc_act_bwd": [_F, _F, _F, _SZ, ctypes.c_int],
             "orc_lerp": [_F, ctypes.c_float, ctypes.c_float, _F, _SZ],
             "orc_clamp": [_F, ctypes.c_float, ctypes.c_float, _F, _SZ],
             "orc_gather_f32": [_F, _SZ, _I, _F, _SZ],
@@ -170,6 +171,13 @@ def wise(x, fn: int) -> np.ndarray:
     z = np.empty_like(x)
     lib().orc_wise(_f(x), _f(z), x.size, fn)
     return z
+
+
+def act_bwd(y, dy, act: int) -> np.ndarray:
+    y, dy = _c32(y), _c32(dy)
+    dx = np.empty_like(y)
+    lib().orc_act_bwd(_f(y), _f(dy), _f(dx), y.size, act)
+    return dx
 
 
 def lerp(x, v1: float, v2: float) -> np.ndarray:

@@ -92,3 +92,21 @@ def test_cpp_host_layer_builds_and_links():
                          text=True)
     assert out.returncode == 0, out.stderr
     assert os.path.exists(os.path.join(root, "tests", "cpp", "host_api_test"))
+    assert os.path.exists(os.path.join(root, "tests", "cpp", "graph_test"))
+
+
+def test_pool_core_bookkeeping():
+    """The caching pool's bookkeeping (cortexmind_amd/csrc/pool.hpp) over a
+    host backend, built with AddressSanitizer/UBSan: size classes, same-stream
+    reuse, no cross-stream reuse, foreign/double frees, release-and-retry on
+    out-of-memory, stream teardown, no leaks."""
+    import os
+    import subprocess
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = subprocess.run(["make", "-s", "-C", os.path.join(root, "tests", "cpp")], capture_output=True, text=True)
+    assert out.returncode == 0, out.stderr
+    run = subprocess.run([os.path.join(root, "tests", "cpp", "pool_core_test")], capture_output=True, text=True,
+                         timeout=60)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert "ALL OK" in run.stdout

@@ -174,3 +174,17 @@ def test_sgd(hip, orc, n, off):
     dw, dg = dev(w, off), dev(gr, off)
     call("cxm_sgd_f32", dw.ptr, dg.ptr, np.float32(0.01), n, None)
     assert bits_equal(dw.numpy(), orc.sgd(w, gr, 0.01))
+
+
+@pytest.mark.parametrize("act", [ACT_RELU, ACT_SIGMOID, ACT_TANH])
+@pytest.mark.parametrize("n,off", [(1, 0), (4099, 0), (1 << 20, 0), (1031, 1)])
+def test_act_bwd_bit_exact(hip, orc, act, n, off):
+    """dx = dy * act'(y) from the saved output (what a ReLU/sigmoid/tanh
+    GradientFlow runs): one rounded factor, one product, bit-exact."""
+    x = SplitMix64(700 + n + act).normal((n,), 0.0, 2.0)
+    y = orc.unary(x, act)
+    y[: min(n, 3)] = np.array([0.0, -0.0, 1.0], np.float32)[: min(n, 3)]  # relu' at 0 and -0 is 0
+    dy = SplitMix64(800 + n).normal((n,), 0.0, 1.0)
+    d_y, d_dy, d_dx = dev(y, off), dev(dy, off), empty((n,), offset_floats=off)
+    call("cxm_act_bwd_f32", d_y.ptr, d_dy.ptr, d_dx.ptr, n, act, None)
+    assert bits_equal(d_dx.numpy(), orc.act_bwd(y, dy, act))

@@ -546,3 +546,17 @@ def test_var_closed_forms(orc):
     assert orc.reduce_flat("var", f32([-3.0, 3.0] * 64))[0] == 9.0  # +-c: c^2
     assert orc.reduce_flat("stdv", f32([-3.0, 3.0] * 64))[0] == 3.0
     assert np.isnan(orc.reduce_flat("var", np.zeros(0, np.float32))[0])  # 0/0
+
+
+@pytest.mark.parametrize("act", [1, 2, 3])
+def test_act_bwd_is_affine_bwd_with_unit_scale(orc, act):
+    # dx of the (already pinned) affine backward with scale 1 is dy*act'(y)
+    # exactly (the product with 1 is exact), so act_bwd must match it bit for bit
+    rng = np.random.default_rng(60 + act)
+    x = rng.normal(size=(7, 33)).astype(np.float32)
+    y = orc.unary(x, act) if act != 1 else np.maximum(x, 0).astype(np.float32)
+    dy = rng.normal(size=(7, 33)).astype(np.float32)
+    dx_aff, _, _ = orc.affine_act_bwd(x, np.ones(33, np.float32), y, dy, act)
+    assert np.array_equal(orc.act_bwd(y, dy, act), dx_aff)
+    if act == 1:  # relu' = [y > 0]: zero where y <= 0, dy elsewhere
+        assert np.array_equal(orc.act_bwd(y, dy, act), np.where(y > 0, dy, np.float32(0) * dy))
