@@ -22,6 +22,7 @@ E_TOO_LARGE = -2
 E_NO_DEVICE = -3
 
 OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_MAX, OP_MIN, OP_POW = range(7)
+DT_F32, DT_BF16, DT_F16 = range(3)
 (FN_SQUARE, FN_SQRT, FN_RSQRT, FN_LOG, FN_EXP, FN_ERF, FN_SIN, FN_COS, FN_ABS, FN_NEG, FN_RCP,
  FN_INVERSE, FN_SIGN) = range(13)
 ACT_NONE, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_EXP = range(5)
@@ -60,6 +61,11 @@ SIGNATURES = {
     "cxm_event_destroy": [_P],
     "cxm_release_workspaces": [],
     "cxm_act_bwd_f32": [_P, _P, _P, _SZ, _I, _P],
+    "cxm_convert": [_P, _I, _P, _I, _SZ, _P],
+    "cxm_binary_t": [_P, _P, _P, _SZ, _I, _I, _P],
+    "cxm_scalar_t": [_P, _F, _P, _SZ, _I, _I, _P],
+    "cxm_unary_t": [_P, _P, _SZ, _I, _I, _P],
+    "cxm_wise_t": [_P, _P, _SZ, _I, _I, _P],
     "cxm_pool_alloc": [ctypes.POINTER(_P), _SZ, _P],
     "cxm_pool_free": [_P],
     "cxm_pool_release": [],

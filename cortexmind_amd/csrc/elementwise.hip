@@ -16,6 +16,7 @@
 // followed by a rounded sum, never an fma.  ReLU is an explicit select
 // (0 > t ? 0 : t), matching _mm256_max_ps(0, t) for -0.0 and NaN.
 #include "cxm_common.hpp"
+#include "ops.hpp"
 
 namespace cxm {
 namespace {
@@ -33,53 +34,14 @@ __device__ __forceinline__ float bin(int op, float a, float b) {
 }
 
 template <int OP>
-__device__ __forceinline__ float bin_t(float a, float b) {
-    if constexpr (OP == CXM_OP_ADD) return a + b;
-    else if constexpr (OP == CXM_OP_SUB) return a - b;
-    else if constexpr (OP == CXM_OP_MUL) return a * b;
-    else if constexpr (OP == CXM_OP_DIV) return a / b;
-    else if constexpr (OP == CXM_OP_MAX) return a > b ? a : b;
-    else if constexpr (OP == CXM_OP_MIN) return a < b ? a : b;
-    else return powf(a, b);
-}
-
-template <int OP>
 __device__ __forceinline__ float4 bin4(float4 a, float4 b) {
     return make_float4(bin_t<OP>(a.x, b.x), bin_t<OP>(a.y, b.y), bin_t<OP>(a.z, b.z),
                        bin_t<OP>(a.w, b.w));
 }
 
-// relu: functions.hpp:372-374; sigmoid: functions.hpp:405-411 (1/(1+exp(-x)));
-// tanh: functions.hpp:381-383; exp: functions.hpp:186-188.
-template <int ACT>
-__device__ __forceinline__ float act(float t) {
-    if constexpr (ACT == CXM_ACT_RELU) return 0.0f > t ? 0.0f : t;
-    else if constexpr (ACT == CXM_ACT_SIGMOID) {
-        const float e = expf(-t);
-        const float d = 1.0f + e;
-        return 1.0f / d;
-    } else if constexpr (ACT == CXM_ACT_TANH) return tanhf(t);
-    else if constexpr (ACT == CXM_ACT_EXP) return expf(t);
-    else return t;
-}
-
 template <int ACT>
 __device__ __forceinline__ float4 act4(float4 t) {
     return make_float4(act<ACT>(t.x), act<ACT>(t.y), act<ACT>(t.z), act<ACT>(t.w));
-}
-
-// Derivative factor from the saved output y (one rounding per operation):
-// relu' = y > 0, sigmoid' = y*(1-y), tanh' = 1 - y*y.
-template <int ACT>
-__device__ __forceinline__ float dact(float y) {
-    if constexpr (ACT == CXM_ACT_RELU) return y > 0.0f ? 1.0f : 0.0f;
-    else if constexpr (ACT == CXM_ACT_SIGMOID) {
-        const float t = 1.0f - y;
-        return y * t;
-    } else if constexpr (ACT == CXM_ACT_TANH) {
-        const float t = y * y;
-        return 1.0f - t;
-    } else return 1.0f;
 }
 
 // Grid for a flat streaming kernel: enough workgroups to fill 256 CUs

@@ -1,0 +1,95 @@
+// Scalar operators shared by the fp32 and the 16-bit elementwise kernels:
+// binary ops, activations and their derivative factors, and the unary math
+// functions of the elementwise surface.  Each is the per-element
+// expression the reference's operators apply (cited where defined); the
+// library is built with -ffp-contract=off, so no product is fused into a
+// sum unless fmaf says so.
+#pragma once
+
+#include "cxm_common.hpp"
+
+namespace cxm {
+
+template <int OP>
+__device__ __forceinline__ float bin_t(float a, float b) {
+    if constexpr (OP == CXM_OP_ADD) return a + b;
+    else if constexpr (OP == CXM_OP_SUB) return a - b;
+    else if constexpr (OP == CXM_OP_MUL) return a * b;
+    else if constexpr (OP == CXM_OP_DIV) return a / b;
+    else if constexpr (OP == CXM_OP_MAX) return a > b ? a : b;
+    else if constexpr (OP == CXM_OP_MIN) return a < b ? a : b;
+    else return powf(a, b);
+}
+
+// relu: functions.hpp:372-374; sigmoid: functions.hpp:405-411 (1/(1+exp(-x)));
+// tanh: functions.hpp:381-383; exp: functions.hpp:186-188.
+template <int ACT>
+__device__ __forceinline__ float act(float t) {
+    if constexpr (ACT == CXM_ACT_RELU) return 0.0f > t ? 0.0f : t;
+    else if constexpr (ACT == CXM_ACT_SIGMOID) {
+        const float e = expf(-t);
+        const float d = 1.0f + e;
+        return 1.0f / d;
+    } else if constexpr (ACT == CXM_ACT_TANH) return tanhf(t);
+    else if constexpr (ACT == CXM_ACT_EXP) return expf(t);
+    else return t;
+}
+
+// Derivative factor from the saved output y (one rounding per operation):
+// relu' = y > 0, sigmoid' = y*(1-y), tanh' = 1 - y*y.
+template <int ACT>
+__device__ __forceinline__ float dact(float y) {
+    if constexpr (ACT == CXM_ACT_RELU) return y > 0.0f ? 1.0f : 0.0f;
+    else if constexpr (ACT == CXM_ACT_SIGMOID) {
+        const float t = 1.0f - y;
+        return y * t;
+    } else if constexpr (ACT == CXM_ACT_TANH) {
+        const float t = y * y;
+        return 1.0f - t;
+    } else return 1.0f;
+}
+
+// ------------------------------------------------ unary math functions
+// (nv::ElementWise / avx2::wise: Operations/kernel_ops.cuh:73-284)
+
+struct FSquare { __device__ float operator()(float x) const { return x * x; } };
+struct FSqrt { __device__ float operator()(float x) const { return __builtin_sqrtf(x); } };
+struct FRsqrt {
+    __device__ float operator()(float x) const {
+        const float r = __builtin_sqrtf(x);
+        return 1.0f / r;
+    }
+};
+struct FLog { __device__ float operator()(float x) const { return logf(x); } };
+struct FExp { __device__ float operator()(float x) const { return expf(x); } };
+struct FErf { __device__ float operator()(float x) const { return erff(x); } };
+struct FSin { __device__ float operator()(float x) const { return sinf(x); } };
+struct FCos { __device__ float operator()(float x) const { return cosf(x); } };
+struct FAbs { __device__ float operator()(float x) const { return fabsf(x); } };
+struct FNeg { __device__ float operator()(float x) const { return -x; } };
+struct FRcp { __device__ float operator()(float x) const { return 1.0f / x; } };
+// (x > 0) - (x < 0): Operations/kernel_ops.cuh:268-274
+struct FSign {
+    __device__ float operator()(float x) const {
+        return static_cast<float>(static_cast<int>(x > 0.0f) - static_cast<int>(x < 0.0f));
+    }
+};
+// fma(t, b - a, a) with a = x, b = v1, t = v2: functions.hpp:271-274
+struct FLerp {
+    float v1, v2;
+    __device__ float operator()(float x) const {
+        const float d = v1 - x;
+        return fmaf(v2, d, x);
+    }
+};
+// min(max(x, lo), hi) with the SIMD operand rule max(a, b) = a > b ? a : b,
+// min(a, b) = a < b ? a : b: functions.hpp:332-335
+struct FClamp {
+    float lo, hi;
+    __device__ float operator()(float x) const {
+        const float m = x > lo ? x : lo;
+        return m < hi ? m : hi;
+    }
+};
+
+}  // namespace cxm

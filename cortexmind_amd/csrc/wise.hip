@@ -14,49 +14,10 @@
 // CUDA build compiles with --use_fast_math; the results here are at least as
 // accurate as either.
 #include "cxm_common.hpp"
+#include "ops.hpp"
 
 namespace cxm {
 namespace {
-
-struct FSquare { __device__ float operator()(float x) const { return x * x; } };
-struct FSqrt { __device__ float operator()(float x) const { return __builtin_sqrtf(x); } };
-struct FRsqrt {
-    __device__ float operator()(float x) const {
-        const float r = __builtin_sqrtf(x);
-        return 1.0f / r;
-    }
-};
-struct FLog { __device__ float operator()(float x) const { return logf(x); } };
-struct FExp { __device__ float operator()(float x) const { return expf(x); } };
-struct FErf { __device__ float operator()(float x) const { return erff(x); } };
-struct FSin { __device__ float operator()(float x) const { return sinf(x); } };
-struct FCos { __device__ float operator()(float x) const { return cosf(x); } };
-struct FAbs { __device__ float operator()(float x) const { return fabsf(x); } };
-struct FNeg { __device__ float operator()(float x) const { return -x; } };
-struct FRcp { __device__ float operator()(float x) const { return 1.0f / x; } };
-// (x > 0) - (x < 0): Operations/kernel_ops.cuh:268-274
-struct FSign {
-    __device__ float operator()(float x) const {
-        return static_cast<float>(static_cast<int>(x > 0.0f) - static_cast<int>(x < 0.0f));
-    }
-};
-// fma(t, b - a, a) with a = x, b = v1, t = v2: functions.hpp:271-274
-struct FLerp {
-    float v1, v2;
-    __device__ float operator()(float x) const {
-        const float d = v1 - x;
-        return fmaf(v2, d, x);
-    }
-};
-// min(max(x, lo), hi) with the SIMD operand rule max(a, b) = a > b ? a : b,
-// min(a, b) = a < b ? a : b: functions.hpp:332-335
-struct FClamp {
-    float lo, hi;
-    __device__ float operator()(float x) const {
-        const float m = x > lo ? x : lo;
-        return m < hi ? m : hi;
-    }
-};
 
 template <class F>
 __global__ __launch_bounds__(kBlock) void k_map_any(F f, const float *x, float *z, size_t n) {

@@ -71,6 +71,12 @@ typedef struct ihipEvent_t *cxm_event_t;   /* a hipEvent_t */
 #define CXM_FN_INVERSE 11
 #define CXM_FN_SIGN 12
 
+/* Element types of the dtype-generic entry points (Type/dtype.hpp's
+ * Float32 / BFloat16 / Float16). */
+#define CXM_DT_F32 0
+#define CXM_DT_BF16 1
+#define CXM_DT_F16 2
+
 /* Human-readable text for a status code (never NULL). */
 const char *cxm_error_string(int status);
 
@@ -237,6 +243,27 @@ int cxm_gather_f32(const float *x, size_t x_n, const int32_t *idx, float *z, siz
                    cxm_stream_t s);
 int cxm_gather_i32(const int32_t *x, size_t x_n, const int32_t *idx, int32_t *z, size_t n,
                    cxm_stream_t s);
+
+/* ---------------------------------------------------- 16-bit element types
+ * convert() (Tools/cast.cpp:7-90): dst[i] = src[i] between CXM_DT_F32,
+ * CXM_DT_BF16 and CXM_DT_F16.  bf16 -> f32 and f16 -> f32 are exact;
+ * f32 -> bf16 rounds to nearest-even (cast.cpp:55-68's bias formula; NaN
+ * stays a quiet NaN); f32 -> f16 is the IEEE round-to-nearest-even
+ * conversion (_mm256_cvtps_ph).  16-bit data are arrays of uint16. */
+int cxm_convert(void *dst, int dst_dtype, const void *src, int src_dtype, size_t n, cxm_stream_t s);
+/* The elementwise surface for any CXM_DT_*: binary (ops ADD..POW), scalar,
+ * activation (RELU..EXP) and math (CXM_FN_*).  CXM_DT_F32 runs the *_f32
+ * entry points above.  bf16/f16 (the reference's CPU kernel_t, wise.cpp:
+ * 17-52, and its CUDA __nv_bfloat162 / __half2 kernels, Kernels/unary.cuh:
+ * 42-90, binary.cuh:41-89, scalar.cuh:69-130): each element is widened to
+ * fp32, the fp32 operator applied, and the result rounded once to nearest-
+ * even, which is the correctly rounded 16-bit result for + - * / and sqrt.
+ * A scalar operand is first rounded to the 16-bit type, as the CUDA path
+ * passes it. */
+int cxm_binary_t(const void *x, const void *y, void *z, size_t n, int op, int dtype, cxm_stream_t s);
+int cxm_scalar_t(const void *x, float value, void *z, size_t n, int op, int dtype, cxm_stream_t s);
+int cxm_unary_t(const void *x, void *z, size_t n, int act, int dtype, cxm_stream_t s);
+int cxm_wise_t(const void *x, void *z, size_t n, int fn, int dtype, cxm_stream_t s);
 
 /* Fused y = act(x * scale[j] + bias[j]) over [m, n]: Broadcast::row::mul then
  * Broadcast::row::add in place (broadcast.cpp:206-216, 230-240), then the

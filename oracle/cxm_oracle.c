@@ -31,6 +31,7 @@
  *    oracle skips such a block.  NaN inputs are outside the parity contract.
  */
 #include <float.h>
+#include <immintrin.h>
 #include <math.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -603,6 +604,47 @@ void orc_gather_f32(const float *x, size_t xn, const int32_t *idx, float *z, siz
 void orc_gather_i32(const int32_t *x, size_t xn, const int32_t *idx, int32_t *z, size_t n) {
     for (size_t i = 0; i < n; ++i)
         z[i] = (idx[i] >= 0 && (size_t)idx[i] < xn) ? x[idx[i]] : INT32_MIN;
+}
+
+/* ------------------------------------------------------ 16-bit conversions */
+
+enum { ORC_DT_F32 = 0, ORC_DT_BF16 = 1, ORC_DT_F16 = 2 };
+
+/* convert(float*, const bfloat16*) (Tools/cast.cpp:7-23): bits << 16. */
+static inline float bf16_to_f32(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* convert(bfloat16*, const float*) (cast.cpp:55-78): u + 0x7FFF + lsb, >> 16
+ * (round to nearest-even).  Deliberate deviation: NaN stays a quiet NaN
+ * (the formula turns NaNs with a small payload into infinity). */
+static inline uint16_t f32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* convert(float*, const half*) / convert(half*, const float*) (cast.cpp:25-41,
+ * 80-90): _mm256_cvtph_ps / _mm256_cvtps_ph(_MM_FROUND_TO_NEAREST_INT), here
+ * their scalar F16C forms. */
+static inline float f16_to_f32(uint16_t h) { return _cvtsh_ss(h); }
+static inline uint16_t f32_to_f16(float f) { return (uint16_t)_cvtss_sh(f, _MM_FROUND_TO_NEAREST_INT); }
+
+void orc_convert(void *dst, int ddt, const void *src, int sdt, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        float v;
+        if (sdt == ORC_DT_F32) v = ((const float *)src)[i];
+        else if (sdt == ORC_DT_BF16) v = bf16_to_f32(((const uint16_t *)src)[i]);
+        else v = f16_to_f32(((const uint16_t *)src)[i]);
+        if (ddt == ORC_DT_F32) ((float *)dst)[i] = v;
+        else if (ddt == ORC_DT_BF16) ((uint16_t *)dst)[i] = f32_to_bf16(v);
+        else ((uint16_t *)dst)[i] = f32_to_f16(v);
+    }
 }
 
 /* ----------------------------------------------------------- activations */

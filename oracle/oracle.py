@@ -20,6 +20,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libcxm_oracle.so")
 
 ADD, SUB, MUL, DIV, MAX, MIN, POW = range(7)
+DT_F32, DT_BF16, DT_F16 = range(3)
 (FN_SQUARE, FN_SQRT, FN_RSQRT, FN_LOG, FN_EXP, FN_ERF, FN_SIN, FN_COS, FN_ABS, FN_NEG, FN_RCP,
  FN_INVERSE, FN_SIGN) = range(13)
 ACT_NONE, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_EXP = range(5)
@@ -64,6 +65,7 @@ def lib() -> ctypes.CDLL:
             "orc_scalar": [_F, ctypes.c_float, _F, _SZ, ctypes.c_int],
             "orc_unary": [_F, _F, _SZ, ctypes.c_int],
             "orc_wise": [_F, _F, _SZ, ctypes.c_int],
+            "orc_convert": [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, _SZ],
             "orc_act_bwd": [_F, _F, _F, _SZ, ctypes.c_int],
             "orc_lerp": [_F, ctypes.c_float, ctypes.c_float, _F, _SZ],
             "orc_clamp": [_F, ctypes.c_float, ctypes.c_float, _F, _SZ],
@@ -171,6 +173,32 @@ def wise(x, fn: int) -> np.ndarray:
     z = np.empty_like(x)
     lib().orc_wise(_f(x), _f(z), x.size, fn)
     return z
+
+
+def convert(src, src_dt: int, dst_dt: int) -> np.ndarray:
+    """Tools/cast.cpp convert(): float32 <-> bf16/f16 (16-bit data as uint16)."""
+    src = np.ascontiguousarray(src, dtype=np.float32 if src_dt == DT_F32 else np.uint16)
+    dst = np.empty(src.shape, np.float32 if dst_dt == DT_F32 else np.uint16)
+    lib().orc_convert(dst.ctypes.data, dst_dt, src.ctypes.data, src_dt, src.size)
+    return dst
+
+
+def binary_t(x, y, op: int, dt: int) -> np.ndarray:
+    """16-bit binary op: widen, fp32 op, round once (wise.cpp:17-52 kernel_t)."""
+    return convert(binary(convert(x, dt, DT_F32), convert(y, dt, DT_F32), op), DT_F32, dt)
+
+
+def scalar_t(x, value: float, op: int, dt: int) -> np.ndarray:
+    v = convert(convert(np.array([value], np.float32), DT_F32, dt), dt, DT_F32)[0]
+    return convert(scalar(convert(x, dt, DT_F32), v, op), DT_F32, dt)
+
+
+def unary_t(x, act: int, dt: int) -> np.ndarray:
+    return convert(unary(convert(x, dt, DT_F32), act), DT_F32, dt)
+
+
+def wise_t(x, fn: int, dt: int) -> np.ndarray:
+    return convert(wise(convert(x, dt, DT_F32), fn), DT_F32, dt)
 
 
 def act_bwd(y, dy, act: int) -> np.ndarray:

@@ -560,3 +560,41 @@ def test_act_bwd_is_affine_bwd_with_unit_scale(orc, act):
     assert np.array_equal(orc.act_bwd(y, dy, act), dx_aff)
     if act == 1:  # relu' = [y > 0]: zero where y <= 0, dy elsewhere
         assert np.array_equal(orc.act_bwd(y, dy, act), np.where(y > 0, dy, np.float32(0) * dy))
+
+
+# ------------------------------------------------------------ 16-bit casts
+
+def test_bf16_f16_widening_exhaustive(orc):
+    # every 16-bit pattern: bf16 widens to bits << 16; f16 widens as numpy's IEEE float16
+    h = np.arange(65536, dtype=np.uint16)
+    wb = orc.convert(h, orc.DT_BF16, orc.DT_F32)
+    assert np.array_equal(wb.view(np.uint32), h.astype(np.uint32) << 16)
+    wf = orc.convert(h, orc.DT_F16, orc.DT_F32)
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(wf), nan) and np.array_equal(wf[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    # round trips are the identity on non-NaN patterns
+    assert np.array_equal(orc.convert(wb, orc.DT_F32, orc.DT_BF16)[~np.isnan(wb)], h[~np.isnan(wb)])
+    assert np.array_equal(orc.convert(wf, orc.DT_F32, orc.DT_F16)[~nan], h[~nan])
+
+
+def test_f32_to_bf16_round_to_nearest_even(orc):
+    # exact integer rounding of the 32-bit pattern to its top 16 bits, ties to even
+    rng = np.random.default_rng(71)
+    u = rng.integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32)
+    u = u[(u & 0x7FFFFFFF) < 0x7F800000]  # finite
+    u = np.concatenate([u, np.array([0x3F808000, 0x3F818000, 0x3F807FFF, 0x7F7FFFFF, 0x00008000], np.uint32)])
+    f = u.view(np.float32)
+    got = orc.convert(f, orc.DT_F32, orc.DT_BF16).astype(np.uint64)
+    hi, lo = u.astype(np.uint64) >> 16, u.astype(np.uint64) & 0xFFFF
+    exp = hi + ((lo > 0x8000) | ((lo == 0x8000) & (hi & 1 == 1))).astype(np.uint64)
+    assert np.array_equal(got, exp)  # 0x7F7FFFFF rounds up to 0x7F80 (inf), as RNE does
+    nanb = orc.convert(np.array([np.nan, -np.nan], np.float32), orc.DT_F32, orc.DT_BF16)
+    assert np.all(np.isnan(orc.convert(nanb, orc.DT_BF16, orc.DT_F32)))
+
+
+def test_f32_to_f16_matches_numpy(orc):
+    rng = np.random.default_rng(72)
+    f = np.concatenate([rng.normal(0, 100, 100000), rng.normal(0, 1e-5, 10000),
+                        [65504.0, 65520.0, 1e6, -1e6, 6e-8, 0.0, -0.0, np.inf, -np.inf]]).astype(np.float32)
+    assert np.array_equal(orc.convert(f, orc.DT_F32, orc.DT_F16), f.astype(np.float16).view(np.uint16))
