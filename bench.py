@@ -153,10 +153,10 @@ def wl_c4(E, D):
     big = 4 * x.size
     S = E.softmax
     ops = [
-        Op("softmax_fwd", "k_sm_fwd_part+apply", lambda k: S.forward(X[k % nset], Y[k % nset], r, c), 2 * big),
-        Op("logsoftmax_fwd", "k_sm_fwd_part+apply<log>", lambda k: S.forward(X[k % nset], Y[k % nset], r, c, log=True), 2 * big),
-        Op("softmax_bwd", "k_sm_bwd_part+apply", lambda k: S.backward(Y[k % nset], G[k % nset], dX[k % nset], r, c), 3 * big),
-        Op("logsoftmax_bwd", "k_sm_bwd_part+apply<log>", lambda k: S.backward(Y[k % nset], G[k % nset], dX[k % nset], r, c, log=True), 3 * big),
+        Op("softmax_fwd", "k_sm_fwd_x", lambda k: S.forward(X[k % nset], Y[k % nset], r, c), 2 * big),
+        Op("logsoftmax_fwd", "k_sm_fwd_x<log>", lambda k: S.forward(X[k % nset], Y[k % nset], r, c, log=True), 2 * big),
+        Op("softmax_bwd", "k_sm_bwd_x", lambda k: S.backward(Y[k % nset], G[k % nset], dX[k % nset], r, c), 3 * big),
+        Op("logsoftmax_bwd", "k_sm_bwd_x<log>", lambda k: S.backward(Y[k % nset], G[k % nset], dX[k % nset], r, c, log=True), 3 * big),
     ]
     desc = {"workload": "C4 long-row softmax/log-softmax fwd+bwd fp32 [64,131072] N(0,1)*8, 10% -inf",
             "shape": [r, c], "rotating_sets": nset}

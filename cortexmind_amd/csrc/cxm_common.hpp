@@ -45,6 +45,19 @@ struct Workspace {
 };
 int get_workspace(cxm_stream_t s, size_t counters, size_t scratch_bytes, Workspace *ws);
 
+// Exchange region of the single-pass long-row softmax, one per (device,
+// stream), kept apart from the workspace scratch (which other kernels
+// overwrite).  Row r owns a header of kCtr words at hdr + r * kCtr (word 0:
+// arrival ticket, word 1: epoch) and kXMaxSegs slot pairs at
+// slots + r * kXMaxSegs * 2; each slot is a 64-bit (value, tag) word.
+// Zero-filled when allocated; grows on demand (after a stream sync).
+constexpr unsigned kXMaxSegs = 64;
+struct Exchange {
+    unsigned *hdr;
+    unsigned long long *slots;
+};
+int get_exchange(cxm_stream_t s, size_t rows, Exchange *x);
+
 // Returns the caching pool's blocks of a stream to the device (pool.hip).
 int pool_drop_stream(cxm_stream_t s);
 

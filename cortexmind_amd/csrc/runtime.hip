@@ -1,5 +1,6 @@
 // Device, memory, stream and event entry points of the C ABI, plus the
-// per-(device, stream) workspace the multi-pass kernels use.
+// per-(device, stream) workspace the multi-pass kernels use and the
+// exchange region of the single-pass long-row softmax.
 //
 // Replaces the reference's device pool and copies: ForgeChunk
 // (source/CortexMind/framework/Memory/forge.cu:13-122, one 128 MiB
@@ -25,7 +26,15 @@ struct WsEntry {
     void *base = nullptr;
     size_t counters = 0;
     size_t scratch_bytes = 0;
+    void *xbase = nullptr;  // exchange region (never shared with other kernels' scratch)
+    size_t xrows = 0;
 };
+
+void free_entry(WsEntry &w) {
+    if (w.base) (void)hipFree(w.base);
+    if (w.xbase) (void)hipFree(w.xbase);
+    w.base = w.xbase = nullptr;
+}
 
 std::mutex g_ws_mu;
 std::map<std::pair<int, cxm_stream_t>, WsEntry> g_ws;
@@ -72,6 +81,41 @@ int get_workspace(cxm_stream_t s, size_t counters, size_t scratch_bytes, Workspa
     ws->counters_n = w.counters;
     ws->scratch = static_cast<unsigned *>(w.base) + w.counters * cxm::kCtr;
     ws->scratch_bytes = w.scratch_bytes;
+    return CXM_OK;
+}
+
+int get_exchange(cxm_stream_t s, size_t rows, Exchange *x) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return st(e);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    WsEntry &w = g_ws[{dev, s}];
+    if (w.xbase == nullptr || w.xrows < rows) {
+        size_t nr = rows < 64 ? 64 : rows;
+        if (w.xrows > nr) nr = w.xrows;
+        if (w.xbase != nullptr) {
+            e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(s));
+            if (e != hipSuccess) return st(e);
+            e = hipFree(w.xbase);
+            w.xbase = nullptr;
+            w.xrows = 0;
+            if (e != hipSuccess) return st(e);
+        }
+        const size_t bytes = nr * (kCtr * sizeof(unsigned) + kXMaxSegs * 2 * sizeof(unsigned long long));
+        void *p = nullptr;
+        e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) return st(e);
+        // all-zero: epoch 0, tickets 0, every slot tagged 0
+        e = hipMemsetAsync(p, 0, bytes, reinterpret_cast<hipStream_t>(s));
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            return st(e);
+        }
+        w.xbase = p;
+        w.xrows = nr;
+    }
+    x->hdr = static_cast<unsigned *>(w.xbase);
+    x->slots = reinterpret_cast<unsigned long long *>(static_cast<unsigned *>(w.xbase) + w.xrows * kCtr);
     return CXM_OK;
 }
 
@@ -181,7 +225,7 @@ int cxm_stream_destroy(cxm_stream_t s) {
         for (auto it = g_ws.begin(); it != g_ws.end();) {
             if (it->first.second == s) {
                 (void)hipStreamSynchronize(reinterpret_cast<hipStream_t>(s));
-                if (it->second.base) (void)hipFree(it->second.base);
+                free_entry(it->second);
                 it = g_ws.erase(it);
             } else {
                 ++it;
@@ -229,6 +273,7 @@ int cxm_release_workspaces(void) {
         (void)hipSetDevice(kv.first.first);
         hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(kv.first.second));
         if (e == hipSuccess && kv.second.base) e = hipFree(kv.second.base);
+        if (e == hipSuccess && kv.second.xbase) e = hipFree(kv.second.xbase);
         if (e != hipSuccess && rc == CXM_OK) rc = st(e);
     }
     g_ws.clear();

@@ -12,16 +12,21 @@
 // in place of the division: at most one rounding apart); the order in
 // which s is summed differs.
 //
-// Three kernel families by row length:
+// Kernel families by row length:
 //  * wave per row, row in registers (cols <= 4096, cols % 4 == 0): one pass
 //    over HBM, DPP wave reductions, no LDS;
-//  * split rows (long rows): pass 1 reduces each 4096-element segment to
+//  * long rows (up to 64 segments of 8192, up to 8192 rows): one pass, each
+//    workgroup holds a segment in registers and the workgroups of a row
+//    exchange partials through device memory (see the single-pass section);
+//  * longer rows or more rows: pass 1 reduces each 4096-element segment to
 //    (max m_b, sum_b exp(x - m_b)) [forward] or to its partial dot product
 //    [backward]; pass 2 combines the row's partials in segment order
 //    (S = sum_b s_b * exp(m_b - M)), re-reads its segment and writes;
 //  * any shape or alignment: wave per row, three sweeps over the row.
 // The running max starts from -FLT_MAX, as reduce::max does, so an
 // all -inf row (or segment) never forms (-inf) - (-inf).
+#include <atomic>
+
 #include "cxm_common.hpp"
 
 namespace cxm {
@@ -320,6 +325,286 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_apply(const float *__restrict
     }
 }
 
+// ------------------------------------------- single pass, long rows
+//
+// A row of up to kXMaxSegs segments of kXNV float4 per thread (8192 floats)
+// is read once: workgroup (row, b) keeps its segment in registers, reduces
+// it to a partial, publishes the partial in its slot of the row's exchange
+// record, reads the partials of the other segments of its row, combines all
+// of them in segment order (so every workgroup of the row gets the same
+// row statistic, bit for bit), and writes its segment.  HBM traffic is one
+// read and one write, where the two-pass form reads the input twice.
+//
+// No cooperative launch and no grid-wide barrier: a slot is valid when its
+// tag equals the row's epoch + 1.  Every workgroup reads the epoch before it
+// takes its arrival ticket; the workgroup that takes the row's last ticket
+// advances the epoch (and resets the ticket) after all of them have read it,
+// so a slot written by any earlier call never carries the current tag.  The
+// wait for a peer's slot is bounded (g_xwait polls); a peer not seen by then
+// is not waited for: its partial is recomputed from the input with the same
+// arithmetic as the owner's, so the result is the same bit for bit, only
+// slower.  Every workgroup therefore finishes whatever the dispatch order
+// or residency of its peers.
+
+constexpr int kXNV = 8;
+constexpr size_t kXSeg = static_cast<size_t>(kBlock) * 4 * kXNV;  // floats per segment
+constexpr size_t kXRowsMax = 8192;
+constexpr unsigned kXWaitDefault = 1u << 16;  // polls (each a device round trip plus a short sleep)
+std::atomic<unsigned> g_xwait{kXWaitDefault};
+
+__device__ __forceinline__ unsigned long long xld(const unsigned long long *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void xst(unsigned long long *p, float v, unsigned tag) {
+    __hip_atomic_store(p, (static_cast<unsigned long long>(tag) << 32) | __builtin_bit_cast(unsigned, v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float xval(unsigned long long u) {
+    return __builtin_bit_cast(float, static_cast<unsigned>(u));
+}
+__device__ __forceinline__ unsigned xtag(unsigned long long u) { return static_cast<unsigned>(u >> 32); }
+
+// Thread 0: read the row's epoch, then take an arrival ticket (the read has
+// returned before the ticket is issued).  Returns the ticket; *tag = epoch+1.
+__device__ __forceinline__ unsigned x_arrive(unsigned *h, unsigned *tag) {
+    const unsigned e = __hip_atomic_load(h + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    *tag = e + 1;
+    return __hip_atomic_fetch_add(h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Thread 0 of the workgroup holding the row's last ticket, after its work.
+__device__ __forceinline__ void x_leave(unsigned *h, unsigned ticket, unsigned segs, unsigned tag) {
+    if (ticket == segs - 1) {
+        __hip_atomic_store(h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(h + 1, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Lanes b < segs of wave 0 wait (bounded) for slot word `w` of segment b;
+// returns the mask of segments not seen.  The own segment is not read.
+template <int W>
+__device__ __forceinline__ unsigned long long x_gather(const unsigned long long *sl, unsigned segs,
+                                                       unsigned own, unsigned tag, unsigned limit,
+                                                       float (*out)[kXMaxSegs]) {
+    const unsigned b = threadIdx.x;
+    bool miss = false;
+    if (b < segs && b != own) {
+        unsigned long long u[W];
+        for (unsigned tries = 0;; ++tries) {
+            bool ok = true;
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                u[w] = xld(sl + 2 * b + w);
+                ok = ok && xtag(u[w]) == tag;
+            }
+            if (ok) break;
+            if (tries >= limit) {
+                miss = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+#pragma unroll
+        for (int w = 0; w < W; ++w) out[w][b] = xval(u[w]);
+    }
+    return __ballot(miss);
+}
+
+__device__ __forceinline__ float max4(float m, float4 v) { return vmax(vmax(vmax(vmax(m, v.x), v.y), v.z), v.w); }
+__device__ __forceinline__ float4 exp4(float4 v, float m) {
+    return make_float4(expf(v.x - m), expf(v.y - m), expf(v.z - m), expf(v.w - m));
+}
+__device__ __forceinline__ float sum4(float4 e) { return (e.x + e.y) + (e.z + e.w); }
+// sum(dy*y) partial, one rounding order pinned by explicit fmas
+__device__ __forceinline__ float dot4(float r, float4 g, float4 y) {
+    return fmaf(g.w, y.w, fmaf(g.z, y.z, fmaf(g.y, y.y, fmaf(g.x, y.x, r))));
+}
+
+// Forward.  Softmax keeps e = exp(x - m_t) (m_t the thread's max) and writes
+// e * (exp(m_t - M) * (1/S)); log-softmax keeps x and writes (x - M) - log S.
+template <bool LOG>
+__global__ __launch_bounds__(kBlock) void k_sm_fwd_x(const float *__restrict__ x, float *__restrict__ y,
+                                                     size_t cols, unsigned segs, unsigned *hdr,
+                                                     unsigned long long *slots, unsigned limit) {
+    constexpr int NV = kXNV;
+    __shared__ float lds[kWavesPerBlock];
+    __shared__ float part[2][kXMaxSegs];
+    __shared__ unsigned long long s_miss;
+    __shared__ unsigned s_tag;
+    const size_t row = blockIdx.x / segs;
+    const unsigned seg = blockIdx.x - static_cast<unsigned>(row) * segs;
+    const float *__restrict__ xr = x + row * cols;
+    const size_t n4 = (cols - static_cast<size_t>(seg) * kXSeg) / 4;
+    const float4 ninf = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    float4 v[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
+        v[k] = i < n4 ? ld4_stream(xr + seg * kXSeg + 4 * i) : ninf;
+    }
+    unsigned *h = hdr + row * kCtr;
+    unsigned ticket = 0, tag = 0;
+    if (threadIdx.x == 0) {
+        ticket = x_arrive(h, &tag);
+        s_tag = tag;
+    }
+    float mt = kLowest;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) mt = max4(mt, v[k]);
+    float st = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const float4 e = exp4(v[k], mt);
+        st += sum4(e);
+        if constexpr (!LOG) v[k] = e;
+    }
+    const float Mb = block_reduce<MaxOp, kBlock>(mt, lds);
+    const float Sb = block_reduce<SumOp, kBlock>(st * expf(mt - Mb), lds);
+    tag = s_tag;  // written before the barriers above
+    unsigned long long *sl = slots + row * kXMaxSegs * 2;
+    if (threadIdx.x == 0) {
+        xst(sl + 2 * seg, Mb, tag);
+        xst(sl + 2 * seg + 1, Sb, tag);
+        part[0][seg] = Mb;
+        part[1][seg] = Sb;
+    }
+    if (threadIdx.x < kWave) {
+        const unsigned long long miss = x_gather<2>(sl, segs, seg, tag, limit, part);
+        if (threadIdx.x == 0) s_miss = miss;
+    }
+    __syncthreads();
+    // peers not seen: recompute their partials from the input, same arithmetic
+    for (unsigned long long miss = s_miss; miss; miss &= miss - 1) {
+        const unsigned b = static_cast<unsigned>(__builtin_ctzll(miss));
+        const float *xb = xr + b * kXSeg;
+        const size_t nb = (cols - static_cast<size_t>(b) * kXSeg) / 4;
+        float m = kLowest;
+#pragma unroll 1
+        for (int k = 0; k < NV; ++k) {
+            const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
+            m = max4(m, i < nb ? ld4(xb + 4 * i) : ninf);
+        }
+        float s = 0.0f;
+#pragma unroll 1
+        for (int k = 0; k < NV; ++k) {
+            const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
+            s += sum4(exp4(i < nb ? ld4(xb + 4 * i) : ninf, m));
+        }
+        const float M1 = block_reduce<MaxOp, kBlock>(m, lds);
+        const float S1 = block_reduce<SumOp, kBlock>(s * expf(m - M1), lds);
+        if (threadIdx.x == 0) {
+            part[0][b] = M1;
+            part[1][b] = S1;
+        }
+    }
+    __syncthreads();
+    const bool has = threadIdx.x < segs;
+    const float M = block_reduce<MaxOp, kBlock>(has ? part[0][threadIdx.x] : kLowest, lds);
+    const float S =
+        block_reduce<SumOp, kBlock>(has ? part[1][threadIdx.x] * expf(part[0][threadIdx.x] - M) : 0.0f, lds);
+    float *__restrict__ ys = y + row * cols + seg * kXSeg;
+    if constexpr (LOG) {
+        const float ls = logf(S);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
+            if (i < n4)
+                st4_stream(ys + 4 * i, make_float4((v[k].x - M) - ls, (v[k].y - M) - ls, (v[k].z - M) - ls,
+                                                   (v[k].w - M) - ls));
+        }
+    } else {
+        const float f = expf(mt - M) * (1.0f / S);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
+            if (i < n4) st4_stream(ys + 4 * i, make_float4(v[k].x * f, v[k].y * f, v[k].z * f, v[k].w * f));
+        }
+    }
+    if (threadIdx.x == 0) x_leave(h, ticket, segs, tag);
+}
+
+// Backward: partial r_b = sum(dy*y) or sum(dy) per segment, r = sum_b r_b
+// in segment order, then dx as the wave kernel writes it.
+template <bool LOG>
+__global__ __launch_bounds__(kBlock) void k_sm_bwd_x(const float *__restrict__ y, const float *__restrict__ dy,
+                                                     float *__restrict__ dx, size_t cols, unsigned segs,
+                                                     unsigned *hdr, unsigned long long *slots,
+                                                     unsigned limit) {
+    constexpr int NV = kXNV;
+    __shared__ float lds[kWavesPerBlock];
+    __shared__ float part[1][kXMaxSegs];
+    __shared__ unsigned long long s_miss;
+    __shared__ unsigned s_tag;
+    const size_t row = blockIdx.x / segs;
+    const unsigned seg = blockIdx.x - static_cast<unsigned>(row) * segs;
+    const size_t rbase = row * cols;
+    const size_t base = rbase + seg * kXSeg;
+    const size_t n4 = (cols - static_cast<size_t>(seg) * kXSeg) / 4;
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 yv[NV], gv[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
+        const bool in = i < n4;
+        yv[k] = in ? ld4_stream(y + base + 4 * i) : zero;
+        gv[k] = in ? ld4_stream(dy + base + 4 * i) : zero;
+    }
+    unsigned *h = hdr + row * kCtr;
+    unsigned ticket = 0, tag = 0;
+    if (threadIdx.x == 0) {
+        ticket = x_arrive(h, &tag);
+        s_tag = tag;
+    }
+    float r = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) r = LOG ? r + sum4(gv[k]) : dot4(r, gv[k], yv[k]);
+    const float rb = block_reduce<SumOp, kBlock>(r, lds);
+    tag = s_tag;
+    unsigned long long *sl = slots + row * kXMaxSegs * 2;
+    if (threadIdx.x == 0) {
+        xst(sl + 2 * seg, rb, tag);
+        part[0][seg] = rb;
+    }
+    if (threadIdx.x < kWave) {
+        const unsigned long long miss = x_gather<1>(sl, segs, seg, tag, limit, part);
+        if (threadIdx.x == 0) s_miss = miss;
+    }
+    __syncthreads();
+    for (unsigned long long miss = s_miss; miss; miss &= miss - 1) {
+        const unsigned b = static_cast<unsigned>(__builtin_ctzll(miss));
+        const size_t bb = rbase + b * kXSeg;
+        const size_t nb = (cols - static_cast<size_t>(b) * kXSeg) / 4;
+        float q = 0.0f;
+#pragma unroll 1
+        for (int k = 0; k < NV; ++k) {
+            const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
+            const bool in = i < nb;
+            const float4 g = in ? ld4(dy + bb + 4 * i) : zero;
+            if constexpr (LOG) q = q + sum4(g);
+            else q = dot4(q, g, in ? ld4(y + bb + 4 * i) : zero);
+        }
+        const float q1 = block_reduce<SumOp, kBlock>(q, lds);
+        if (threadIdx.x == 0) part[0][b] = q1;
+    }
+    __syncthreads();
+    const float R = block_reduce<SumOp, kBlock>(threadIdx.x < segs ? part[0][threadIdx.x] : 0.0f, lds);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
+        if (i >= n4) continue;
+        float4 o;
+        if constexpr (LOG) {
+            o.x = gv[k].x - expf(yv[k].x) * R; o.y = gv[k].y - expf(yv[k].y) * R;
+            o.z = gv[k].z - expf(yv[k].z) * R; o.w = gv[k].w - expf(yv[k].w) * R;
+        } else {
+            o.x = yv[k].x * (gv[k].x - R); o.y = yv[k].y * (gv[k].y - R);
+            o.z = yv[k].z * (gv[k].z - R); o.w = yv[k].w * (gv[k].w - R);
+        }
+        st4_stream(dx + base + 4 * i, o);
+    }
+    if (threadIdx.x == 0) x_leave(h, ticket, segs, tag);
+}
+
 // --------------------------------------------------- generic (any shape)
 
 // Wave per row, three sweeps; handles every column count and alignment.
@@ -453,6 +738,41 @@ int sm_bwd_wave(const float *y, const float *dy, float *dx, size_t rows, size_t 
 // Long rows: split when a row exceeds the wave kernel's register capacity.
 bool use_split(size_t cols) { return cols > kWaveRowMax; }
 
+// Single pass when the row has at most kXMaxSegs segments and the exchange
+// region stays small (rows * 1.25 KiB).
+bool use_x(size_t rows, size_t cols) { return rows <= kXRowsMax && (cols + kXSeg - 1) / kXSeg <= kXMaxSegs; }
+
+int sm_fwd_x(const float *x, float *y, size_t rows, size_t cols, int log_mode, cxm_stream_t st) {
+    const unsigned segs = static_cast<unsigned>((cols + kXSeg - 1) / kXSeg);
+    Exchange xc;
+    const int rc = get_exchange(st, rows, &xc);
+    if (rc) return rc;
+    const dim3 grid(static_cast<unsigned>(rows * segs));
+    const unsigned lim = g_xwait.load(std::memory_order_relaxed);
+    if (log_mode)
+        hipLaunchKernelGGL(k_sm_fwd_x<true>, grid, dim3(kBlock), 0, hs(st), x, y, cols, segs, xc.hdr, xc.slots, lim);
+    else
+        hipLaunchKernelGGL(k_sm_fwd_x<false>, grid, dim3(kBlock), 0, hs(st), x, y, cols, segs, xc.hdr, xc.slots, lim);
+    return launch_status();
+}
+
+int sm_bwd_x(const float *y, const float *dy, float *dx, size_t rows, size_t cols, int log_mode,
+             cxm_stream_t st) {
+    const unsigned segs = static_cast<unsigned>((cols + kXSeg - 1) / kXSeg);
+    Exchange xc;
+    const int rc = get_exchange(st, rows, &xc);
+    if (rc) return rc;
+    const dim3 grid(static_cast<unsigned>(rows * segs));
+    const unsigned lim = g_xwait.load(std::memory_order_relaxed);
+    if (log_mode)
+        hipLaunchKernelGGL(k_sm_bwd_x<true>, grid, dim3(kBlock), 0, hs(st), y, dy, dx, cols, segs, xc.hdr, xc.slots,
+                           lim);
+    else
+        hipLaunchKernelGGL(k_sm_bwd_x<false>, grid, dim3(kBlock), 0, hs(st), y, dy, dx, cols, segs, xc.hdr,
+                           xc.slots, lim);
+    return launch_status();
+}
+
 template <int NV>
 int sm_fwd_split(const float *x, float *y, size_t rows, size_t cols, int log_mode, cxm_stream_t st) {
     constexpr size_t L = kBlock * 4 * NV;
@@ -513,6 +833,7 @@ int softmax_fwd(const float *x, float *y, size_t rows, size_t cols, int log_mode
     }
     if (!use_split(cols))
         return log_mode ? sm_fwd_wave<true>(x, y, rows, cols, s) : sm_fwd_wave<false>(x, y, rows, cols, s);
+    if (use_x(rows, cols)) return sm_fwd_x(x, y, rows, cols, log_mode, st);
     return sm_fwd_split<kSegNV>(x, y, rows, cols, log_mode, st);
 }
 
@@ -531,6 +852,7 @@ int softmax_bwd(const float *y, const float *dy, float *dx, size_t rows, size_t 
     if (!use_split(cols))
         return log_mode ? sm_bwd_wave<true>(y, dy, dx, rows, cols, s)
                         : sm_bwd_wave<false>(y, dy, dx, rows, cols, s);
+    if (use_x(rows, cols)) return sm_bwd_x(y, dy, dx, rows, cols, log_mode, st);
     return sm_bwd_split<kSegNV>(y, dy, dx, rows, cols, log_mode, st);
 }
 
@@ -549,6 +871,12 @@ int cxm_softmax_fwd_f32(const float *x, float *y, size_t rows, size_t cols, int 
 int cxm_softmax_bwd_f32(const float *y, const float *dy, float *dx, size_t rows, size_t cols,
                         int log_mode, cxm_stream_t s) {
     return softmax_bwd(y, dy, dx, rows, cols, log_mode, s);
+}
+
+int cxm_softmax_wait_limit(unsigned polls, unsigned *previous) {
+    const unsigned old = g_xwait.exchange(polls);
+    if (previous) *previous = old;
+    return CXM_OK;
 }
 
 int cxm_softmax_xent_f32(const float *logits, const int32_t *labels, float *loss, float *dlogits,
