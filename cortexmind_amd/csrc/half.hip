@@ -12,12 +12,7 @@
 // scalar operands are first rounded to the 16-bit type, as the CUDA path
 // passes them.
 //
-// Conversions (cast.cpp:7-90): bf16 -> f32 is a 16-bit shift; f32 -> bf16
-// rounds to nearest-even by adding 0x7FFF + lsb, like the reference's SIMD
-// body (cast.cpp:55-68), except that NaN stays a quiet NaN (the reference's
-// formula turns a NaN with a small payload into infinity); f16 <-> f32 is
-// the IEEE conversion (v_cvt_f16_f32 / v_cvt_f32_f16, round to
-// nearest-even), as _mm256_cvtps_ph / _mm256_cvtph_ps.
+// Conversions (cast.cpp:7-90): see half.hpp.
 //
 // Vector path: 16-byte aligned pointers, eight 16-bit elements (one
 // 128-bit load) per thread, one 256-thread workgroup per 2048 elements,
@@ -25,30 +20,11 @@
 #include <cstring>
 
 #include "cxm_common.hpp"
+#include "half.hpp"
 #include "ops.hpp"
 
 namespace cxm {
 namespace {
-
-template <int DT>
-struct H;
-template <>
-struct H<CXM_DT_BF16> {
-    __device__ static float load(uint16_t h) { return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16); }
-    __device__ static uint16_t store(float f) {
-        uint32_t u = __builtin_bit_cast(uint32_t, f);
-        if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-        u += 0x7fffu + ((u >> 16) & 1u);
-        return static_cast<uint16_t>(u >> 16);
-    }
-};
-template <>
-struct H<CXM_DT_F16> {
-    __device__ static float load(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
-    __device__ static uint16_t store(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
-};
-
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t *p) { return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p)); }
 __device__ __forceinline__ void st16(uint16_t *p, u32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(p)); }

@@ -161,6 +161,13 @@ class matrix_t:
         """Row-major Xz[xN, zN] = Xx[xN, yN] * Xy[yN, zN] (matrix.hpp:119)."""
         call("cxm_matmul_f32", _p(Xx), _p(Xy), _p(Xz), xN, yN, zN, _s(stream))
 
+    @staticmethod
+    def matmul_t(Xx, Xy, Xz, xN, yN, zN, dtype, stream=None):
+        """matmul for a CXM_DT_* dtype: nv::Matrix::matmul's bf16 / fp16
+        branches (Engine/CUDA/matrix.cu:112-159) on 16-bit element arrays,
+        fp32 accumulation, one rounding to the 16-bit output."""
+        call("cxm_matmul_t", _p(Xx), _p(Xy), _p(Xz), xN, yN, zN, dtype, _s(stream))
+
 
 class ScalarOp:
     """avx2::ScalarOp (Engine/AVX2/scalar.cpp:89-119): Xz = Xx op value."""

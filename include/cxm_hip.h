@@ -316,6 +316,16 @@ int cxm_matmul_f32(const float *a, const float *b, float *c, size_t xN, size_t y
 int cxm_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t k, size_t n,
                  int trans_a, int trans_b, const float *bias, int act, const float *gate,
                  cxm_stream_t s);
+/* matmul for any CXM_DT_*: nv::Matrix::matmul (Engine/CUDA/matrix.cu:112-159)
+ * with its per-dtype cublasGemmEx (BlasTraits, matrix.cu:18-37).  bf16 and
+ * fp16 operands and output (16-bit element arrays), fp32 accumulation on
+ * v_mfma_f32_32x32x16_{bf16,f16}, one round-to-nearest-even at the end (the
+ * reference's fp16 form accumulates in fp16).  CXM_DT_F32 runs cxm_matmul_f32.
+ * cxm_gemm_t adds the transposed forms of cxm_gemm_f32 (no epilogue). */
+int cxm_matmul_t(const void *a, const void *b, void *c, size_t xN, size_t yN, size_t zN, int dtype,
+                 cxm_stream_t s);
+int cxm_gemm_t(const void *a, const void *b, void *c, size_t m, size_t k, size_t n, int trans_a,
+               int trans_b, int dtype, cxm_stream_t s);
 
 /* ----------------------------------------------------------- training step
  * Softmax cross-entropy on logits [b, c] with int32 labels in [0, c):

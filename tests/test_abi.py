@@ -93,6 +93,7 @@ def test_cpp_host_layer_builds_and_links():
     assert out.returncode == 0, out.stderr
     assert os.path.exists(os.path.join(root, "tests", "cpp", "host_api_test"))
     assert os.path.exists(os.path.join(root, "tests", "cpp", "graph_test"))
+    assert os.path.exists(os.path.join(root, "tests", "cpp", "nv_api_test"))
 
 
 def test_pool_core_bookkeeping():
