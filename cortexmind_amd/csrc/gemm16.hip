@@ -9,16 +9,26 @@
 // accurate of the two; results differ from the exact product of the 16-bit
 // inputs by the fp32 accumulation error plus the final rounding.
 //
-// Tiling: a 256-thread workgroup (four waves, one per SIMD) computes a
+// Three kernels, chosen by shape (gemm16() below), all accumulating each
+// output over k in the same order (32x32x16 blocks in k order), so they
+// give the same bits:
+//  * k_gemm16_ring: 256x256 tiles, four LDS stages filled by direct
+//    global-to-LDS loads; for M, N multiples of 256 and K of 128 (operands
+//    not stored k-contiguous are transposed into the workspace first);
+//  * k_gemm16_big: 256x256 tiles with register staging, any shape;
+//  * k_gemm16: 128x128 tiles, for grids too small for 256x256 tiles.
+// MFMA operand layout (32x32x16): lane l supplies A[l%32][8*(l/32) .. +7]
+// and B[8*(l/32) .. +7][l%32]; accumulator register r of lane l holds
+// C[8*(r/4) + 4*(l/32) + r%4][l%32].
+//
+// k_gemm16: a 256-thread workgroup (four waves, one per SIMD) computes a
 // 128x128 tile of C; each wave owns 64x64 = 2x2 MFMA tiles of 32x32
 // (64 accumulator registers per lane).  K advances in steps of 64 through
 // double-buffered LDS tiles stored with k contiguous (As[m][k], Bs[n][k],
 // row stride 72 elements = 144 bytes), so one ds_read_b128 is one MFMA
-// operand: lane l supplies A[l%32][8*(l/32) .. +7] and B[8*(l/32) .. +7][l%32]
-// of a 32x32x16 block; accumulator register r of lane l holds
-// C[8*(r/4) + 4*(l/32) + r%4][l%32].
+// operand.
 //
-// Staging through registers:
+// Staging through registers (k_gemm16, k_gemm16_big):
 //  * operand stored with k contiguous (A [m,k], or B^T stored [n,k]): one
 //    128-bit load of 8 k and one 128-bit LDS write per chunk;
 //  * operand stored with the tile row contiguous (B [k,n], or A^T stored
@@ -229,7 +239,510 @@ __global__ __launch_bounds__(kHThreads) void k_gemm16(const uint16_t *__restrict
         }
 }
 
+// ------------------------------------------------ 256x256 workgroup tiles
+//
+// Four waves, each 128x128 of C = 4x4 MFMA tiles of 32x32 (256 fp32
+// accumulators per lane, in the accumulation registers), so a k block of 16
+// costs 8 fragment reads for 16 MFMAs, half the LDS traffic per MFMA of the
+// 64x64 waves above.  BK = 64; the 16-byte k groups of an LDS row are
+// XOR-swizzled with the row's 8-row index (group g of row r sits at
+// g ^ ((r / 8) % 8)): fragment reads stay single ds_read_b128s, and the
+// 64-bit writes of the transposed staging, whose lanes walk along rows,
+// spread over the banks instead of all landing on the same 16 bytes.
+constexpr int kG_BM = 256, kG_BN = 256, kG_BK = 64, kG_KP = kG_BK + 8;
+
+__device__ __forceinline__ int swz(int r, int g) { return g ^ ((r >> 3) & 7); }
+
+template <bool KC>
+struct StageBig {
+    static constexpr int kRegs = 8;
+    int r, k;  // KC: first row (chunk s adds 32 rows), k group * 8; else: r8 block base row, first k of block 0
+    __device__ __forceinline__ void init(int tid) {
+        if constexpr (KC) {
+            r = tid / 8;
+            k = (tid % 8) * 8;
+        } else {
+            r = (tid % 32) * 8;  // block s: k = 4 * (tid / 32 + 8 * s)
+            k = (tid / 32) * 4;
+        }
+    }
+    template <bool V>
+    __device__ __forceinline__ void load(const uint16_t *__restrict__ X, size_t r0, size_t k0, size_t R, size_t Kd,
+                                         u32x4 (&v)[kRegs]) const {
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+        if constexpr (KC) {
+#pragma unroll
+            for (int s = 0; s < kRegs; ++s) {
+                const size_t rg = r0 + r + 32 * s, kg = k0 + k;
+                if (rg >= R || kg >= Kd) {
+                    v[s] = zero;
+                } else {
+                    const uint16_t *p = X + rg * Kd + kg;
+                    v[s] = V ? *reinterpret_cast<const u32x4 *>(p) : ld8_part(p, Kd - kg);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < kRegs; ++s) {  // block s / 4, k row s % 4
+                const size_t rg = r0 + r, kg = k0 + k + 32 * (s / 4) + (s % 4);
+                if (rg >= R || kg >= Kd) {
+                    v[s] = zero;
+                } else {
+                    const uint16_t *p = X + kg * R + rg;
+                    v[s] = V ? *reinterpret_cast<const u32x4 *>(p) : ld8_part(p, R - rg);
+                }
+            }
+        }
+    }
+    __device__ __forceinline__ void store(uint16_t (*Xs)[kG_KP], const u32x4 (&v)[kRegs]) const {
+        if constexpr (KC) {
+#pragma unroll
+            for (int s = 0; s < kRegs; ++s) {
+                const int row = r + 32 * s;
+                *reinterpret_cast<u32x4 *>(&Xs[row][8 * swz(row, k / 8)]) = v[s];
+            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int kk = k + 32 * b;  // 4 k of this block: group kk / 8, half (kk / 4) % 2
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const u32x4 *q = v + 4 * b;
+                    const u32x2 lo = {(q[0][w] & 0xffffu) | (q[1][w] << 16), (q[2][w] & 0xffffu) | (q[3][w] << 16)};
+                    const u32x2 hi = {(q[0][w] >> 16) | (q[1][w] & 0xffff0000u), (q[2][w] >> 16) | (q[3][w] & 0xffff0000u)};
+                    const int r0 = r + 2 * w, r1 = r0 + 1;
+                    *reinterpret_cast<u32x2 *>(&Xs[r0][8 * swz(r0, kk / 8) + (kk & 4)]) = lo;
+                    *reinterpret_cast<u32x2 *>(&Xs[r1][8 * swz(r1, kk / 8) + (kk & 4)]) = hi;
+                }
+            }
+        }
+    }
+};
+
+// Loads of one staged tile.  CHECKED: rows and k beyond the matrix read as
+// zero (edge tiles, the last partial k step); otherwise every access is in
+// range and the loads are unconditional, so the main loop stays one basic
+// block that the scheduling barriers below can order.
+template <bool KC, bool V, bool CHECKED>
+__device__ __forceinline__ void big_load(const StageBig<KC> &st, const uint16_t *__restrict__ X, size_t r0, size_t k0,
+                                         size_t R, size_t Kd, u32x4 (&v)[8]) {
+    if constexpr (CHECKED) {
+        st.template load<V>(X, r0, k0, R, Kd, v);
+    } else if constexpr (KC) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            v[s] = *reinterpret_cast<const u32x4 *>(X + (r0 + st.r + 32 * s) * Kd + k0 + st.k);
+    } else {
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            v[s] = *reinterpret_cast<const u32x4 *>(X + (k0 + st.k + 32 * (s / 4) + (s % 4)) * R + r0 + st.r);
+    }
+}
+
+// One k step: MFMAs on LDS buffer `buf` with the next block's fragments
+// read during the current block's MFMAs; after block WAT-1 the staged
+// registers `st_a/st_b` go to the other buffer.
+template <int DT, bool TA, bool TB, int WAT>
+__device__ __forceinline__ void big_step(const StageBig<!TA> &sa, const StageBig<TB> &sb, uint16_t (*As)[kG_BM][kG_KP],
+                                         uint16_t (*Bs)[kG_BN][kG_KP], int buf, const u32x4 (&st_a)[8],
+                                         const u32x4 (&st_b)[8], f32x16 (&acc)[4][4], int wm, int wn, int l32,
+                                         int lhi) {
+    constexpr int NB = kG_BK / 16;
+    constexpr int WI = 4, WJ = 4;
+    u32x4 fa[WI], fb[WJ];
+#pragma unroll
+    for (int i = 0; i < WI; ++i) {
+        const int row = wm * 128 + i * 32 + l32;
+        fa[i] = *reinterpret_cast<const u32x4 *>(&As[buf][row][8 * swz(row, lhi)]);
+    }
+#pragma unroll
+    for (int j = 0; j < WJ; ++j) {
+        const int row = wn * 128 + j * 32 + l32;
+        fb[j] = *reinterpret_cast<const u32x4 *>(&Bs[buf][row][8 * swz(row, lhi)]);
+    }
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+        u32x4 na[WI], nb[WJ];
+        if (kb + 1 < NB) {
+#pragma unroll
+            for (int i = 0; i < WI; ++i) {
+                const int row = wm * 128 + i * 32 + l32;
+                na[i] = *reinterpret_cast<const u32x4 *>(&As[buf][row][8 * swz(row, 2 * (kb + 1) + lhi)]);
+            }
+#pragma unroll
+            for (int j = 0; j < WJ; ++j) {
+                const int row = wn * 128 + j * 32 + l32;
+                nb[j] = *reinterpret_cast<const u32x4 *>(&Bs[buf][row][8 * swz(row, 2 * (kb + 1) + lhi)]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < WI; ++i)
+#pragma unroll
+            for (int j = 0; j < WJ; ++j) acc[i][j] = mfma16<DT>(fa[i], fb[j], acc[i][j]);
+        if (kb + 1 == WAT) {
+            // the other buffer was last read before the previous barrier
+            sa.store(As[buf ^ 1], st_a);
+            sb.store(Bs[buf ^ 1], st_b);
+        }
+        if (kb + 1 < NB) {
+#pragma unroll
+            for (int i = 0; i < WI; ++i) fa[i] = na[i];
+#pragma unroll
+            for (int j = 0; j < WJ; ++j) fb[j] = nb[j];
+        }
+    }
+}
+
+// Scheduling of an unchecked step: the next-but-one tile's global loads
+// first, then per k block its MFMAs with the next block's fragment reads
+// between them and, after block WAT-1, the LDS stores of the staged tile
+// (loaded a whole step earlier, so neither the stores nor the register
+// transposes before them wait on memory).
+template <bool TB, int WAT>
+__device__ __forceinline__ void big_schedule() {
+    constexpr int NB = kG_BK / 16;
+    constexpr int kWrites = 8 + (TB ? 8 : 16);
+    __builtin_amdgcn_sched_group_barrier(0x020, 16, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            if (kb + 1 < NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if (kb + 1 == WAT) __builtin_amdgcn_sched_group_barrier(0x200, kWrites, 0);
+    }
+}
+
+// Interior tiles, K a multiple of 2*BK.  A's next tile loads at the top of
+// each step and is stored after block WAT-1 (a plain copy, no arithmetic).
+// B's tiles, which are transposed in registers when B is row-contiguous,
+// load one step earlier: tile t+1 sits in register set (t % 2) during step t
+// while tile t+2 loads into the other set.
+template <int DT, bool TA, bool TB, int WAT>
+__device__ __forceinline__ void big_loop_fast(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, size_t M,
+                                              size_t N, size_t K, size_t m0, size_t n0, const StageBig<!TA> &sa,
+                                              const StageBig<TB> &sb, uint16_t (*As)[kG_BM][kG_KP],
+                                              uint16_t (*Bs)[kG_BN][kG_KP], f32x16 (&acc)[4][4], int wm, int wn,
+                                              int l32, int lhi) {
+    u32x4 ra[8], rb0[8], rb1[8];
+    big_load<TB, true, false>(sb, B, n0, kG_BK, N, K, rb0);  // tile 1 (K >= 2*BK here)
+    for (size_t k0 = 0; k0 < K; k0 += 2 * kG_BK) {
+        {  // even step: tile k0 in buffer 0
+            const size_t ka = k0 + kG_BK;  // < K
+            const size_t kb2 = k0 + 2 * kG_BK < K ? k0 + 2 * kG_BK : k0;
+            big_load<!TA, true, false>(sa, A, m0, ka, M, K, ra);
+            big_load<TB, true, false>(sb, B, n0, kb2, N, K, rb1);
+            big_step<DT, TA, TB, WAT>(sa, sb, As, Bs, 0, ra, rb0, acc, wm, wn, l32, lhi);
+            big_schedule<TB, WAT>();
+            __syncthreads();
+        }
+        {  // odd step: tile k0+BK in buffer 1
+            const size_t ka = k0 + 2 * kG_BK < K ? k0 + 2 * kG_BK : k0;
+            const size_t kb3 = k0 + 3 * kG_BK < K ? k0 + 3 * kG_BK : k0;
+            big_load<!TA, true, false>(sa, A, m0, ka, M, K, ra);
+            big_load<TB, true, false>(sb, B, n0, kb3, N, K, rb0);
+            big_step<DT, TA, TB, WAT>(sa, sb, As, Bs, 1, ra, rb1, acc, wm, wn, l32, lhi);
+            big_schedule<TB, WAT>();
+            __syncthreads();
+        }
+    }
+}
+
+// Edge tiles and any K: checked loads, one register set.
+template <int DT, bool TA, bool TB, bool VA, bool VB, int WAT>
+__device__ __forceinline__ void big_loop_checked(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+                                                 size_t M, size_t N, size_t K, size_t m0, size_t n0,
+                                                 const StageBig<!TA> &sa, const StageBig<TB> &sb,
+                                                 uint16_t (*As)[kG_BM][kG_KP], uint16_t (*Bs)[kG_BN][kG_KP],
+                                                 f32x16 (&acc)[4][4], int wm, int wn, int l32, int lhi) {
+    u32x4 ra[8], rb[8];
+    int buf = 0;
+    for (size_t k0 = 0; k0 < K; k0 += kG_BK) {
+        // the last step reloads its own tile and stores it to the idle buffer
+        const size_t kn = k0 + kG_BK < K ? k0 + kG_BK : k0;
+        big_load<!TA, VA, true>(sa, A, m0, kn, M, K, ra);
+        big_load<TB, VB, true>(sb, B, n0, kn, N, K, rb);
+        big_step<DT, TA, TB, WAT>(sa, sb, As, Bs, buf, ra, rb, acc, wm, wn, l32, lhi);
+        __syncthreads();
+        buf ^= 1;
+    }
+}
+
+template <int DT, bool TA, bool TB, bool VA, bool VB, int WAT>
+__global__ __launch_bounds__(kHThreads) void k_gemm16_big(const uint16_t *__restrict__ A,
+                                                          const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
+                                                          size_t M, size_t N, size_t K, unsigned tiles_n) {
+    constexpr int WI = 4, WJ = 4;
+    __shared__ uint16_t As[2][kG_BM][kG_KP];
+    __shared__ uint16_t Bs[2][kG_BN][kG_KP];
+
+    const unsigned wg = xcd_remap16(blockIdx.x, gridDim.x);
+    const size_t m0 = static_cast<size_t>(wg / tiles_n) * kG_BM;
+    const size_t n0 = static_cast<size_t>(wg % tiles_n) * kG_BN;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l32 = lane & 31, lhi = lane >> 5;
+
+    f32x16 acc[WI][WJ];
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    StageBig<!TA> sa;
+    StageBig<TB> sb;
+    sa.init(tid);
+    sb.init(tid);
+    {
+        u32x4 ra[8], rb[8];
+        sa.template load<VA>(A, m0, 0, M, K, ra);
+        sb.template load<VB>(B, n0, 0, N, K, rb);
+        sa.store(As[0], ra);
+        sb.store(Bs[0], rb);
+    }
+    __syncthreads();
+    // interior tiles with 128-bit loads and K a multiple of 2*BK take the
+    // unchecked, double-staged loop
+    const bool full = VA && VB && m0 + kG_BM <= M && n0 + kG_BN <= N && K % (2 * kG_BK) == 0;
+    if (full)
+        big_loop_fast<DT, TA, TB, WAT>(A, B, M, N, K, m0, n0, sa, sb, As, Bs, acc, wm, wn, l32, lhi);
+    else
+        big_loop_checked<DT, TA, TB, VA, VB, WAT>(A, B, M, N, K, m0, n0, sa, sb, As, Bs, acc, wm, wn, l32, lhi);
+
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ; ++j) {
+            const size_t col = n0 + wn * 128 + j * 32 + l32;
+            if (col >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const size_t row = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * lhi + (r % 4);
+                if (row < M) C[row * N + col] = H<DT>::store(acc[i][j][r]);
+            }
+        }
+}
+
+// ----------------------------------------- NT ring: four LDS stages of BK 32
+//
+// Both operands k-contiguous (A [M,K], B stored as B^T [N,K]), interior
+// tiles only (M, N multiples of 256, K a multiple of 128).  A 256x256
+// workgroup tile, four waves of 128x128 as above, but the k loop runs over
+// a ring of four LDS stages of 32 k (16 KB per operand per stage) filled
+// by global_load_lds_dwordx4 three steps ahead.  Each stage is its own
+// __shared__ array and the loop is unrolled over the ring, so the compiler
+// can tell a stage being read from the stages being filled and does not
+// wait for every outstanding LDS load before each fragment read.
+// A step: MFMAs of k block 0 (the next block's fragments read between
+// them); wait for the next stage's loads and the barrier; issue the loads
+// of the stage freed by the previous step; MFMAs of k block 1 with the next
+// stage's block-0 fragments read between them.
+// Rows of 64 bytes, the four 16-byte groups of row r XOR-keyed by
+// (r / 4) % 4: 16 consecutive rows, one group each, land on 16 distinct
+// 16-byte slots of the 64 banks.
+constexpr int kR_BK = 32;
+constexpr int kR_TILE = 256 * kR_BK;  // elements per operand stage
+
+__device__ __forceinline__ int rkey(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ int roff(int row, int g) { return row * kR_BK + 8 * (g ^ rkey(row)); }
+
+// Loads one 256 x 32 stage of X (k-contiguous, row stride Kd) at rows r0..,
+// k0..: each wave fills 64 rows, 16 per instruction (lane L: row L/4, LDS
+// group L%4, global group (L%4) ^ key).
+__device__ __forceinline__ void ring_issue(const uint16_t *__restrict__ X, size_t r0, size_t k0, size_t Kd,
+                                           uint16_t *stage) {
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const int rr = lane >> 2, p = lane & 3;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int rb = w * 64 + s * 16;
+        const int row = rb + rr;
+        const uint16_t *src = X + (r0 + row) * Kd + k0 + 8 * (p ^ rkey(row));
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(stage + rb * kR_BK), 16, 0,
+                                         0);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void ring_frags(const uint16_t *sa, const uint16_t *sb, int kb, int wm, int wn, int l32,
+                                           int lhi, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        fa[i] = *reinterpret_cast<const u32x4 *>(sa + roff(wm * 128 + i * 32 + l32, 2 * kb + lhi));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        fb[j] = *reinterpret_cast<const u32x4 *>(sb + roff(wn * 128 + j * 32 + l32, 2 * kb + lhi));
+}
+
+template <int DT>
+__device__ __forceinline__ void ring_mfma(const u32x4 (&fa)[4], const u32x4 (&fb)[4], f32x16 (&acc)[4][4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<DT>(fa[i], fb[j], acc[i][j]);
+}
+
+// Step t on stage (sa, sb); (na_s, nb_s) is stage t+1; (fa_s, fb_s) is the
+// stage freed by step t-1, refilled here with tile t+3 (tile kf).
+template <int DT>
+__device__ __forceinline__ void ring_step(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, size_t K,
+                                          size_t m0, size_t n0, size_t kf, const uint16_t *sa, const uint16_t *sb,
+                                          const uint16_t *na_s, const uint16_t *nb_s, uint16_t *fill_a,
+                                          uint16_t *fill_b, u32x4 (&fa)[4], u32x4 (&fb)[4], f32x16 (&acc)[4][4],
+                                          int wm, int wn, int l32, int lhi) {
+    u32x4 ga[4], gb[4];
+    ring_frags<DT>(sa, sb, 1, wm, wn, l32, lhi, ga, gb);  // block 1, during block 0's MFMAs
+    ring_mfma<DT>(fa, fb, acc);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    // the next stage has landed (only the most recent fill may be in flight)
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    __syncthreads();
+    ring_issue(A, m0, kf, K, fill_a);
+    ring_issue(B, n0, kf, K, fill_b);
+    ring_frags<DT>(na_s, nb_s, 0, wm, wn, l32, lhi, fa, fb);  // next step's block 0
+    ring_mfma<DT>(ga, gb, acc);
+    __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+}
+
+// Tile order: the XCD remap gives each XCD a contiguous range of tile ids;
+// inside it, ids walk down GM tile rows before moving one tile column, so
+// the ~32 tiles an XCD runs at once share GM row blocks of A and 32/GM
+// column blocks of B in its L2 (one tile row would share 1 and 32).
+__device__ __forceinline__ void group_tile(unsigned id, unsigned tiles_m, unsigned tiles_n, unsigned gm, unsigned *tm,
+                                           unsigned *tn) {
+    const unsigned per_group = gm * tiles_n;
+    const unsigned group = id / per_group;
+    const unsigned first = group * gm;
+    const unsigned rows = tiles_m - first < gm ? tiles_m - first : gm;
+    const unsigned in = id - group * per_group;
+    *tm = first + in % rows;
+    *tn = in / rows;
+}
+
+template <int DT>
+__global__ __launch_bounds__(kHThreads) void k_gemm16_ring(const uint16_t *__restrict__ A,
+                                                           const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
+                                                           size_t M, size_t N, size_t K, unsigned tiles_n,
+                                                           unsigned gm) {
+    __shared__ __attribute__((aligned(16))) uint16_t a0[kR_TILE], a1[kR_TILE], a2[kR_TILE], a3[kR_TILE];
+    __shared__ __attribute__((aligned(16))) uint16_t b0[kR_TILE], b1[kR_TILE], b2[kR_TILE], b3[kR_TILE];
+    unsigned tm, tn;
+    group_tile(xcd_remap16(blockIdx.x, gridDim.x), static_cast<unsigned>(M / kG_BM), tiles_n, gm, &tm, &tn);
+    const size_t m0 = static_cast<size_t>(tm) * kG_BM;
+    const size_t n0 = static_cast<size_t>(tn) * kG_BN;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l32 = lane & 31, lhi = lane >> 5;
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // K % 128 == 0: tiles 0..T-1, T >= 4.  Tiles beyond T-1 reload tile T-1
+    // into a stage that is never read again.
+    const size_t T = K / kR_BK;
+    auto kt = [&](size_t t) { return (t < T ? t : T - 1) * kR_BK; };
+    ring_issue(A, m0, kt(0), K, a0);
+    ring_issue(B, n0, kt(0), K, b0);
+    ring_issue(A, m0, kt(1), K, a1);
+    ring_issue(B, n0, kt(1), K, b1);
+    ring_issue(A, m0, kt(2), K, a2);
+    ring_issue(B, n0, kt(2), K, b2);
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    __syncthreads();
+    u32x4 fa[4], fb[4];
+    ring_frags<DT>(a0, b0, 0, wm, wn, l32, lhi, fa, fb);
+    for (size_t t = 0; t < T; t += 4) {
+        ring_step<DT>(A, B, K, m0, n0, kt(t + 3), a0, b0, a1, b1, a3, b3, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT>(A, B, K, m0, n0, kt(t + 4), a1, b1, a2, b2, a0, b0, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT>(A, B, K, m0, n0, kt(t + 5), a2, b2, a3, b3, a1, b1, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT>(A, B, K, m0, n0, kt(t + 6), a3, b3, a0, b0, a2, b2, fa, fb, acc, wm, wn, l32, lhi);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const size_t col = n0 + wn * 128 + j * 32 + l32;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const size_t row = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * lhi + (r % 4);
+                C[row * N + col] = H<DT>::store(acc[i][j][r]);
+            }
+        }
+}
+
 inline hipStream_t hs(cxm_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// 16-bit transpose of a row-major [R, Cn] matrix into [Cn, R], R and Cn
+// multiples of 128: a 256-thread workgroup per 128x128 tile.  The tile
+// goes through LDS so that both global sides are coalesced: loads with 16
+// lanes along a row (256 contiguous bytes), then each thread takes an 8x8
+// block from LDS (eight 128-bit reads), transposes it in registers and
+// stores it with 16 lanes along an output row.
+constexpr int kT16 = 128, kT16P = kT16 + 8;
+
+__global__ __launch_bounds__(kHThreads) void k_t16(const uint16_t *__restrict__ X, uint16_t *__restrict__ Y, size_t R,
+                                                  size_t Cn, unsigned tiles_c) {
+    __shared__ __attribute__((aligned(16))) uint16_t t[kT16][kT16P];
+    const size_t r0 = static_cast<size_t>(blockIdx.x / tiles_c) * kT16;
+    const size_t c0 = static_cast<size_t>(blockIdx.x % tiles_c) * kT16;
+    {
+        const int cc = threadIdx.x % 16, rr = threadIdx.x / 16;  // 16 lanes per 256-byte row piece
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int row = rr + 16 * i;
+            *reinterpret_cast<u32x4 *>(&t[row][8 * cc]) =
+                *reinterpret_cast<const u32x4 *>(X + (r0 + row) * Cn + c0 + 8 * cc);
+        }
+    }
+    __syncthreads();
+    const int br = threadIdx.x % 16, bc = threadIdx.x / 16;  // block (br, bc); lanes walk br
+    u32x4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const u32x4 *>(&t[8 * br + i][8 * bc]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        u32x4 o;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const unsigned a = v[2 * w][j / 2], b = v[2 * w + 1][j / 2];
+            o[w] = (j & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+        }
+        *reinterpret_cast<u32x4 *>(Y + (c0 + 8 * bc + j) * R + r0 + 8 * br) = o;
+    }
+}
+
+// Launches k_t16 after checking the shape it assumes.
+int transpose16(const uint16_t *X, uint16_t *Y, size_t R, size_t Cn, hipStream_t s) {
+    if (R % kT16 != 0 || Cn % kT16 != 0 || !aligned16(X) || !aligned16(Y)) return CXM_E_INVALID;
+    const size_t tiles = (R / kT16) * (Cn / kT16);
+    if (tiles > 0x7fffffffu) return CXM_E_TOO_LARGE;
+    hipLaunchKernelGGL(k_t16, dim3(static_cast<unsigned>(tiles)), dim3(kHThreads), 0, s, X, Y, R, Cn,
+                       static_cast<unsigned>(Cn / kT16));
+    return launch_status();
+}
 
 template <int DT, bool TA, bool TB>
 int launch16(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size_t N, size_t K, bool va, bool vb,
@@ -241,6 +754,43 @@ int launch16(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size_t
     return launch_status();
 }
 
+template <int DT, bool TA, bool TB>
+int launch_big(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size_t N, size_t K, bool va, bool vb,
+               dim3 grid, unsigned tn, hipStream_t s) {
+    constexpr int W = 3;
+    if (va && vb) hipLaunchKernelGGL((k_gemm16_big<DT, TA, TB, true, true, W>), grid, dim3(kHThreads), 0, s, A, B, C, M, N, K, tn);
+    else if (va) hipLaunchKernelGGL((k_gemm16_big<DT, TA, TB, true, false, W>), grid, dim3(kHThreads), 0, s, A, B, C, M, N, K, tn);
+    else if (vb) hipLaunchKernelGGL((k_gemm16_big<DT, TA, TB, false, true, W>), grid, dim3(kHThreads), 0, s, A, B, C, M, N, K, tn);
+    else hipLaunchKernelGGL((k_gemm16_big<DT, TA, TB, false, false, W>), grid, dim3(kHThreads), 0, s, A, B, C, M, N, K, tn);
+    return launch_status();
+}
+
+template <int DT, bool TA, bool TB>
+int dispatch16(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size_t N, size_t K, bool va, bool vb,
+               hipStream_t s, int kernel) {
+    if (kernel == 0) {
+        const size_t tn = (N + kH_BN - 1) / kH_BN;
+        return launch16<DT, TA, TB>(A, B, C, M, N, K, va, vb, dim3(static_cast<unsigned>((M + kH_BM - 1) / kH_BM * tn)),
+                                    static_cast<unsigned>(tn), s);
+    }
+    const size_t tn = (N + kG_BN - 1) / kG_BN;
+    return launch_big<DT, TA, TB>(A, B, C, M, N, K, va, vb, dim3(static_cast<unsigned>((M + kG_BM - 1) / kG_BM * tn)),
+                                  static_cast<unsigned>(tn), s);
+}
+
+// Kernel choice:
+//  * at least 128 tiles of 256x256, M and N multiples of 256, K of 128,
+//    16-byte aligned: the NT ring (operands not already k-contiguous are
+//    first transposed into the stream's workspace: 2*2*K*N bytes of
+//    traffic for B of NN, a few percent of the product's time);
+//  * at least 128 tiles of 256x256 otherwise: the 256x256 register-staged
+//    kernel (any shape);
+//  * smaller grids: 128x128 tiles (four times the workgroups).
+// g_gemm16_kernel (tests) forces 0 = 128x128, 1 = 256x256, 2 = ring where
+// the ring's shape conditions hold.
+int g_gemm16_kernel = -1;
+constexpr unsigned kRingGroup = 4;
+
 template <int DT>
 int gemm16(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size_t K, size_t N, bool ta, bool tb,
            cxm_stream_t st) {
@@ -249,13 +799,42 @@ int gemm16(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size_t K
     // 128-bit loads need 16-byte aligned bases and stored rows of a multiple of 8
     const bool va = aligned16(A) && (ta ? M % 8 == 0 : K % 8 == 0);
     const bool vb = aligned16(B) && (tb ? K % 8 == 0 : N % 8 == 0);
-    const dim3 grid(static_cast<unsigned>(tiles_m * tiles_n));
-    const unsigned tn = static_cast<unsigned>(tiles_n);
     hipStream_t s = hs(st);
-    if (!ta && !tb) return launch16<DT, false, false>(A, B, C, M, N, K, va, vb, grid, tn, s);
-    if (ta && !tb) return launch16<DT, true, false>(A, B, C, M, N, K, va, vb, grid, tn, s);
-    if (!ta && tb) return launch16<DT, false, true>(A, B, C, M, N, K, va, vb, grid, tn, s);
-    return launch16<DT, true, true>(A, B, C, M, N, K, va, vb, grid, tn, s);
+    const size_t big_tiles = ((M + kG_BM - 1) / kG_BM) * ((N + kG_BN - 1) / kG_BN);
+    const bool ring_ok = M % kG_BM == 0 && N % kG_BN == 0 && K % (4 * kR_BK) == 0 && aligned16(A) && aligned16(B) &&
+                         aligned16(C);
+    int kernel = big_tiles >= 128 ? (ring_ok ? 2 : 1) : 0;
+    if (g_gemm16_kernel >= 0) kernel = g_gemm16_kernel == 2 && !ring_ok ? 1 : g_gemm16_kernel;
+    if (kernel == 2) {
+        // A as [M,K] and B as B^T [N,K], transposing into the workspace where needed
+        const size_t ta_n = ta ? M * K : 0, tb_n = tb ? 0 : K * N;
+        const uint16_t *Ak = A, *Bk = B;
+        if (ta_n + tb_n) {
+            Workspace ws;
+            const int rc = get_workspace(st, 0, (ta_n + tb_n) * sizeof(uint16_t), &ws);
+            if (rc) return rc;
+            uint16_t *w = static_cast<uint16_t *>(ws.scratch);
+            if (ta) {  // A stored [K, M]
+                const int r = transpose16(A, w, K, M, s);
+                if (r) return r;
+                Ak = w;
+            }
+            if (!tb) {  // B stored [K, N]
+                uint16_t *wb = w + ta_n;
+                const int r = transpose16(B, wb, K, N, s);
+                if (r) return r;
+                Bk = wb;
+            }
+        }
+        const unsigned tn = static_cast<unsigned>(N / kG_BN);
+        hipLaunchKernelGGL(k_gemm16_ring<DT>, dim3(static_cast<unsigned>(big_tiles)), dim3(kHThreads), 0, s, Ak, Bk,
+                           C, M, N, K, tn, kRingGroup);
+        return launch_status();
+    }
+    if (!ta && !tb) return dispatch16<DT, false, false>(A, B, C, M, N, K, va, vb, s, kernel);
+    if (ta && !tb) return dispatch16<DT, true, false>(A, B, C, M, N, K, va, vb, s, kernel);
+    if (!ta && tb) return dispatch16<DT, false, true>(A, B, C, M, N, K, va, vb, s, kernel);
+    return dispatch16<DT, true, true>(A, B, C, M, N, K, va, vb, s, kernel);
 }
 
 }  // namespace
@@ -282,6 +861,12 @@ int cxm_gemm_t(const void *a, const void *b, void *c, size_t m, size_t k, size_t
 int cxm_matmul_t(const void *a, const void *b, void *c, size_t xN, size_t yN, size_t zN, int dtype,
                  cxm_stream_t s) {
     return cxm_gemm_t(a, b, c, xN, yN, zN, 0, 0, dtype, s);
+}
+
+int cxm_gemm16_kernel(int kernel) {
+    if (kernel < -1 || kernel > 2) return CXM_E_INVALID;
+    cxm::g_gemm16_kernel = kernel;
+    return CXM_OK;
 }
 
 }  // extern "C"

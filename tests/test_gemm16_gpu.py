@@ -126,3 +126,48 @@ def test_bad_arguments(hip):
     assert lib().cxm_gemm_t(a.ptr, a.ptr, a.ptr, 4, 0, 4, 0, 0, DT_BF16, None) == E_INVALID
     assert lib().cxm_gemm_t(None, a.ptr, a.ptr, 4, 4, 4, 0, 0, DT_BF16, None) == E_INVALID
     assert lib().cxm_gemm_t(a.ptr, a.ptr, a.ptr, 0, 4, 4, 0, 0, DT_BF16, None) == 0
+
+
+def _kernel(k):
+    call("cxm_gemm16_kernel", k)
+
+
+@pytest.mark.parametrize("dt", DTS, ids=["bf16", "f16"])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_kernels_agree_bitwise(hip, orc, dt, ta, tb):
+    """The 128x128, 256x256 and four-stage direct-to-LDS kernels accumulate
+    each output over k in the same order (32x32x16 MFMA blocks in k
+    order), so they give the same bits; the shape meets the direct-load
+    kernel's conditions (M, N multiples of 256, K of 128), and NN/TN/TT
+    pass through the 16-bit transpose first."""
+    m, k, n = 512, 384, 768
+    g = SplitMix64(77 + 4 * ta + 2 * tb + dt)
+    a16, a64 = rand16(g, (k, m) if ta else (m, k), dt, orc)
+    b16, b64 = rand16(g, (n, k) if tb else (k, n), dt, orc)
+    outs = []
+    try:
+        for kern in (0, 1, 2):
+            _kernel(kern)
+            outs.append(run(a16, b16, m, k, n, dt, ta, tb))
+    finally:
+        _kernel(-1)
+    check(outs[0], a64.T if ta else a64, b64.T if tb else b64, dt, orc)
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("dt", DTS, ids=["bf16", "f16"])
+def test_large_default_path(hip, orc, dt):
+    """4096 x 1024 x 2048 NN: 128 tiles of 256x256, so the automatic choice
+    is the direct-load kernel behind a transpose of B."""
+    m, k, n = 4096, 1024, 2048
+    g = SplitMix64(5150 + dt)
+    a16, a64 = rand16(g, (m, k), dt, orc)
+    b16, b64 = rand16(g, (k, n), dt, orc)
+    check(run(a16, b16, m, k, n, dt), a64, b64, dt, orc)
+
+
+def test_kernel_choice_argument(hip):
+    assert lib().cxm_gemm16_kernel(3) == E_INVALID
+    assert lib().cxm_gemm16_kernel(-2) == E_INVALID
+    assert lib().cxm_gemm16_kernel(-1) == 0
