@@ -58,6 +58,10 @@ struct Exchange {
 };
 int get_exchange(cxm_stream_t s, size_t rows, Exchange *x);
 
+// Polls a waiting workgroup makes for a peer's partial before it computes
+// that partial itself (cxm_exchange_wait_limit).
+unsigned exchange_wait_limit();
+
 // Returns the caching pool's blocks of a stream to the device (pool.hip).
 int pool_drop_stream(cxm_stream_t s);
 

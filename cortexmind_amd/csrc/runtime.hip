@@ -11,6 +11,7 @@
 // aligned memory that the vector kernels rely on.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -35,6 +36,8 @@ void free_entry(WsEntry &w) {
     if (w.xbase) (void)hipFree(w.xbase);
     w.base = w.xbase = nullptr;
 }
+
+std::atomic<unsigned> g_xwait{1u << 16};
 
 std::mutex g_ws_mu;
 std::map<std::pair<int, cxm_stream_t>, WsEntry> g_ws;
@@ -118,6 +121,8 @@ int get_exchange(cxm_stream_t s, size_t rows, Exchange *x) {
     x->slots = reinterpret_cast<unsigned long long *>(static_cast<unsigned *>(w.xbase) + w.xrows * kCtr);
     return CXM_OK;
 }
+
+unsigned exchange_wait_limit() { return g_xwait.load(std::memory_order_relaxed); }
 
 }  // namespace cxm
 
@@ -262,6 +267,12 @@ int cxm_event_elapsed_ms(float *ms, cxm_event_t start, cxm_event_t stop) {
 int cxm_event_destroy(cxm_event_t e) {
     if (!e) return CXM_E_INVALID;
     return st(hipEventDestroy(reinterpret_cast<hipEvent_t>(e)));
+}
+
+int cxm_exchange_wait_limit(unsigned polls, unsigned *previous) {
+    const unsigned old = g_xwait.exchange(polls);
+    if (previous) *previous = old;
+    return CXM_OK;
 }
 
 int cxm_release_workspaces(void) {

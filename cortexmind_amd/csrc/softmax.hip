@@ -25,8 +25,6 @@
 //  * any shape or alignment: wave per row, three sweeps over the row.
 // The running max starts from -FLT_MAX, as reduce::max does, so an
 // all -inf row (or segment) never forms (-inf) - (-inf).
-#include <atomic>
-
 #include "cxm_common.hpp"
 
 namespace cxm {
@@ -340,8 +338,9 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_apply(const float *__restrict
 // takes its arrival ticket; the workgroup that takes the row's last ticket
 // advances the epoch (and resets the ticket) after all of them have read it,
 // so a slot written by any earlier call never carries the current tag.  The
-// wait for a peer's slot is bounded (g_xwait polls); a peer not seen by then
-// is not waited for: its partial is recomputed from the input with the same
+// wait for a peer's slot is bounded (exchange_wait_limit() polls, each a
+// device round trip plus a short sleep); a peer not seen by then is not
+// waited for: its partial is recomputed from the input with the same
 // arithmetic as the owner's, so the result is the same bit for bit, only
 // slower.  Every workgroup therefore finishes whatever the dispatch order
 // or residency of its peers.
@@ -349,8 +348,6 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_apply(const float *__restrict
 constexpr int kXNV = 8;
 constexpr size_t kXSeg = static_cast<size_t>(kBlock) * 4 * kXNV;  // floats per segment
 constexpr size_t kXRowsMax = 8192;
-constexpr unsigned kXWaitDefault = 1u << 16;  // polls (each a device round trip plus a short sleep)
-std::atomic<unsigned> g_xwait{kXWaitDefault};
 
 __device__ __forceinline__ unsigned long long xld(const unsigned long long *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -748,7 +745,7 @@ int sm_fwd_x(const float *x, float *y, size_t rows, size_t cols, int log_mode, c
     const int rc = get_exchange(st, rows, &xc);
     if (rc) return rc;
     const dim3 grid(static_cast<unsigned>(rows * segs));
-    const unsigned lim = g_xwait.load(std::memory_order_relaxed);
+    const unsigned lim = exchange_wait_limit();
     if (log_mode)
         hipLaunchKernelGGL(k_sm_fwd_x<true>, grid, dim3(kBlock), 0, hs(st), x, y, cols, segs, xc.hdr, xc.slots, lim);
     else
@@ -763,7 +760,7 @@ int sm_bwd_x(const float *y, const float *dy, float *dx, size_t rows, size_t col
     const int rc = get_exchange(st, rows, &xc);
     if (rc) return rc;
     const dim3 grid(static_cast<unsigned>(rows * segs));
-    const unsigned lim = g_xwait.load(std::memory_order_relaxed);
+    const unsigned lim = exchange_wait_limit();
     if (log_mode)
         hipLaunchKernelGGL(k_sm_bwd_x<true>, grid, dim3(kBlock), 0, hs(st), y, dy, dx, cols, segs, xc.hdr, xc.slots,
                            lim);
@@ -871,12 +868,6 @@ int cxm_softmax_fwd_f32(const float *x, float *y, size_t rows, size_t cols, int 
 int cxm_softmax_bwd_f32(const float *y, const float *dy, float *dx, size_t rows, size_t cols,
                         int log_mode, cxm_stream_t s) {
     return softmax_bwd(y, dy, dx, rows, cols, log_mode, s);
-}
-
-int cxm_softmax_wait_limit(unsigned polls, unsigned *previous) {
-    const unsigned old = g_xwait.exchange(polls);
-    if (previous) *previous = old;
-    return CXM_OK;
 }
 
 int cxm_softmax_xent_f32(const float *logits, const int32_t *labels, float *loss, float *dlogits,

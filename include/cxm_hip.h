@@ -291,14 +291,14 @@ int cxm_softmax_fwd_f32(const float *x, float *y, size_t rows, size_t cols, int 
  * log-softmax dx = dy - exp(y)*sum(dy). */
 int cxm_softmax_bwd_f32(const float *y, const float *dy, float *dx, size_t rows, size_t cols,
                         int log_mode, cxm_stream_t s);
-/* Rows of 4097..524288 columns (up to 8192 rows) take one pass: the
- * workgroups of a row exchange partial statistics through device memory
- * and each waits at most `polls` polls (default 65536) for a peer before it
- * recomputes that peer's partial from the input itself.  Either way the
- * result is the same bit for bit; 0 makes every workgroup recompute (for
- * tests of that path).  Process-wide; *previous (if not NULL) gets the old
- * value.  No reference counterpart. */
-int cxm_softmax_wait_limit(unsigned polls, unsigned *previous);
+/* Kernels whose workgroups exchange partial results through device memory
+ * -- the one-pass softmax of rows of 4097..524288 columns (up to 8192
+ * rows) -- let a workgroup wait at most `polls` polls (default 65536) for a
+ * peer's partial before it computes that partial from the input itself.  Either way the result is the same bit
+ * for bit; 0 makes every waiting workgroup compute (for tests of that
+ * path).  Process-wide; *previous (if not NULL) gets the old value.  No
+ * reference counterpart. */
+int cxm_exchange_wait_limit(unsigned polls, unsigned *previous);
 
 /* ---------------------------------------------------------------- matmul
  * Row-major C[xN, zN] = A[xN, yN] * B[yN, zN]: matrix_t::matmul

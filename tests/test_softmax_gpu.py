@@ -155,7 +155,7 @@ def test_shapes(hip, orc, shape, log, off):
 
 def _wait_limit(polls):
     old = ctypes.c_uint(0)
-    call("cxm_softmax_wait_limit", polls, ctypes.byref(old))
+    call("cxm_exchange_wait_limit", polls, ctypes.byref(old))
     return old.value
 
 
