@@ -43,6 +43,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, published
 PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 matrix, published
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 matrix, published (no sparsity)
 METRIC = "achieved HBM GB/s (% of peak) for fp32 softmax/reductions on 1 MI355X"
 MLP_FLOP_PER_STEP = 39_174_799_360
 
@@ -52,7 +53,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "more"])
+    p.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "more", "g16"])
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="skip the other workloads")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -65,8 +66,9 @@ def parse():
 class Op:
     """One op of a step: fn(k) launches it on input rotation slot k."""
 
-    def __init__(self, name, kernel, fn, work, unit="B"):
+    def __init__(self, name, kernel, fn, work, unit="B", peak=None):
         self.name, self.kernel, self.fn, self.work, self.unit = name, kernel, fn, work, unit
+        self.peak = peak  # TFLOP/s of the matrix unit this op runs on (FLOP ops); fp32 when None
 
 
 # ---------------------------------------------------------------- workloads
@@ -231,7 +233,59 @@ def wl_more(E, D):
     return ops, desc, (bufs, z1, zf, zi, xs, ys), x
 
 
-WORKLOADS = {"c1": wl_c1, "c2": wl_c2, "c3": wl_c3, "c4": wl_c4, "c5": wl_c5, "more": wl_more}
+def wl_g16(E, D):
+    """bf16 / fp16 matmul (cxm_matmul_t, row-major NN, the CUDA path's 16-bit
+    cublasGemmEx): 8192^3 in both types, 4096^3 and the MLP-like
+    4096x1024x1024 in bf16.  Synthetic U(-1, 1) inputs truncated to 16 bits."""
+    from cortexmind_amd._lib import DT_BF16, DT_F16
+
+    rng = np.random.default_rng(16)
+
+    def rand16(shape, dt):
+        f = rng.random(shape, dtype=np.float32) * 2 - 1
+        if dt == DT_BF16:
+            return D.from_numpy((f.view(np.uint32) >> 16).astype(np.uint16))
+        return D.from_numpy(f.astype(np.float16).view(np.uint16))
+
+    shapes = [("bf16_nn_8192", DT_BF16, 8192, 8192, 8192), ("f16_nn_8192", DT_F16, 8192, 8192, 8192),
+              ("bf16_nn_4096", DT_BF16, 4096, 4096, 4096), ("bf16_nn_4096x1024x1024", DT_BF16, 4096, 1024, 1024)]
+    ops, keep = [], []
+    for name, dt, m, k, n in shapes:
+        a, b, c = rand16((m, k), dt), rand16((k, n), dt), D((m, n), np.uint16)
+        keep += [a, b, c]
+        kern = "k_gemm16_ring+k_t16" if m % 256 == 0 and n % 256 == 0 and (m // 256) * (n // 256) >= 128 else "k_gemm16"
+        ops.append(Op(name, kern, lambda i, a=a, b=b, c=c, m=m, k=k, n=n, dt=dt: E.matrix_t.matmul_t(a, b, c, m, k, n, dt),
+                      2 * m * n * k, unit="FLOP", peak=PEAK_BF16_TFLOPS))
+    desc = {"workload": "bf16/fp16 matmul NN (8192^3 bf16 and fp16, 4096^3 and 4096x1024x1024 bf16)",
+            "ops": [o.name for o in ops], "shapes": [list(s[2:]) for s in shapes]}
+    return ops, desc, tuple(keep), shapes
+
+
+def torch_gemm16(shapes, steps):
+    """torch.matmul (hipBLASLt) on the same shapes, for comparison."""
+    import torch
+
+    out = {}
+    for name, dt, m, k, n in shapes:
+        td = torch.bfloat16 if name.startswith("bf16") else torch.float16
+        a = torch.rand(m, k, device="cuda").to(td)
+        b = torch.rand(k, n, device="cuda").to(td)
+        c = torch.empty(m, n, device="cuda", dtype=td)
+        for _ in range(3):
+            torch.matmul(a, b, out=c)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            torch.matmul(a, b, out=c)
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        out[name] = {"avg_ms": round(ms, 5), "TFLOP/s": round(2 * m * n * k / (ms * 1e-3) / 1e12, 2)}
+    return out
+
+
+WORKLOADS = {"c1": wl_c1, "c2": wl_c2, "c3": wl_c3, "c4": wl_c4, "c5": wl_c5, "more": wl_more, "g16": wl_g16}
 
 
 # ------------------------------------------------------------------ timing
@@ -326,8 +380,9 @@ def run_workload(name, steps, warmup, E, D, Event, sync):
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4)}
     else:
-        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4)}
+        peak = (group[0] if not extra_ops else dom).peak or PEAK_FP32_TFLOPS
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
+                "unit": "TFLOP/s", "frac": round(achieved / peak, 4)}
     tr = read_traffic().get(kern)
     roof.update({"traffic": (tr[0] + tr[1]) if tr else None, "kernel": kern,
                  "avg_launch_ms": round(avg_ms, 5), "algorithmic_per_launch": work})
@@ -336,8 +391,23 @@ def run_workload(name, steps, warmup, E, D, Event, sync):
             "config": desc, "roofline": roof, "per_op": per_op, "host": host}
 
 
+def host_cpu():
+    """lscpu's model name and the host's logical CPU count."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count()
+
+
 def cpu_c2(x, seconds):
-    """Single-thread oracle over whole C2 steps (the same ten reductions)."""
+    """Single-thread oracle over whole C2 steps (the same ten reductions),
+    pinned to one core (the reference path is single-threaded); value is
+    the step's bytes over the median step time."""
     from oracle import oracle
 
     rows, cols = x.shape
@@ -347,21 +417,35 @@ def cpu_c2(x, seconds):
     for op in ("sum", "mean", "max", "argmax"):
         step.append(lambda op=op: oracle.reduce_axis(op, x, 1, rows, cols))
     bytes_step = 2 * (4 * x.size + 4) + 4 * (4 * x.size + 4 * rows) + 4 * (4 * x.size + 4 * cols)
-    for f in step:  # warm-up
-        f()
-    t0 = time.perf_counter()
-    nsteps = 0
-    while True:
-        for f in step:
+    old_aff = None
+    core = None
+    if hasattr(os, "sched_getaffinity"):
+        old_aff = os.sched_getaffinity(0)
+        core = min(old_aff)
+        os.sched_setaffinity(0, {core})
+    try:
+        for f in step:  # warm-up
             f()
-        nsteps += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": round(bytes_step * nsteps / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+        times = []
+        t0 = time.perf_counter()
+        while True:
+            ts = time.perf_counter()
+            for f in step:
+                f()
+            times.append(time.perf_counter() - ts)
+            if len(times) >= 5 and time.perf_counter() - t0 >= seconds:
+                break
+        dt = time.perf_counter() - t0
+    finally:
+        if old_aff is not None:
+            os.sched_setaffinity(0, old_aff)
+    med = float(np.median(times))
+    model, nproc = host_cpu()
+    return {"value": round(bytes_step / med / 1e9, 3), "unit": "GB/s", "cores": 1,
             "kind": "port",
-            "sample": f"{nsteps} whole C2 steps (10 reductions of fp32 [4096,4096]) in {dt:.1f} s, "
-                      f"oracle/cxm_oracle.c -O3 -mavx2 -mfma, 1 thread"}
+            "sample": f"median of {len(times)} whole C2 steps (10 reductions of fp32 [4096,4096]) timed over "
+                      f"{dt:.1f} s, oracle/cxm_oracle.c -O3 -mavx2 -mfma, 1 thread pinned to core {core}",
+            "cpu_model": model, "host_nproc": nproc}
 
 
 def main():
@@ -371,6 +455,17 @@ def main():
                                    "--gpus must be 1", "n_gpus": args.gpus}))
         sys.exit(2)
 
+    torch_ok = False
+    if args.workload == "g16":
+        # torch (for the hipBLASLt comparison) brings its own HIP runtime; it
+        # must initialise before this library's runtime is loaded
+        try:
+            import torch
+
+            torch.cuda.init()
+            torch_ok = torch.cuda.is_available()
+        except Exception:  # the comparison is optional
+            torch_ok = False
     from cortexmind_amd import engine as E
     from cortexmind_amd._lib import call
     from cortexmind_amd.device import DeviceArray as D
@@ -395,7 +490,8 @@ def main():
         "value": round(head["value"], 2), "unit": head["unit"], "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(head["ms_per_step"], 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16/f16" if args.workload == "g16" else "f32",
+        "data": "synthetic",
         "config": head["config"], "roofline": head["roofline"], "per_op": head["per_op"],
         "device": info,
     }
@@ -403,9 +499,11 @@ def main():
         out["frac_of_peak"] = round(head["value"] / PEAK_HBM_GBS, 4)
     if not args.no_cpu and args.workload == "c2":
         out["cpu_baseline"] = cpu_c2(head["host"], args.cpu_seconds)
+    if args.workload == "g16" and torch_ok:
+        out["reference_torch_hipblaslt"] = torch_gemm16(head["host"], args.steps)
     if not args.no_extra:
         wl = {}
-        for name in [w for w in ["c1", "c3", "c4", "c5", "more"] if w != args.workload]:
+        for name in [w for w in ["c1", "c3", "c4", "c5", "more", "g16"] if w != args.workload]:
             r = run_workload(name, max(5, args.steps // 5), 2, E, D, Event, sync)
             wl[name] = {"workload": r["config"]["workload"], "value": round(r["value"], 2),
                         "unit": r["unit"], "ms_per_step": round(r["ms_per_step"], 5),
