@@ -376,10 +376,10 @@ struct BcastL {
         if (!rowmap4_grid(m, n / 4, &grid, &tpr)) return CXM_E_TOO_LARGE;
         if (row_mode)
             hipLaunchKernelGGL(k_rowmap4<RowBcastF<OP>>, dim3(grid), dim3(kBlock), 0, s, RowBcastF<OP>{y}, x, z,
-                               n / 4, tpr);
+                               m, n / 4, tpr);
         else
             hipLaunchKernelGGL(k_rowmap4<ColBcastF<OP>>, dim3(grid), dim3(kBlock), 0, s, ColBcastF<OP>{y}, x, z,
-                               n / 4, tpr);
+                               m, n / 4, tpr);
         return launch_status();
     }
 };
@@ -414,7 +414,7 @@ int affine_fwd_t(const float *x, const float *scale, const float *bias, float *y
     if (n % 4 == 0 && aligned16(x) && aligned16(scale) && aligned16(bias) && aligned16(y) &&
         rowmap4_grid(m, n / 4, &grid, &tpr)) {
         hipLaunchKernelGGL(k_rowmap4<AffineF<ACT>>, dim3(grid), dim3(kBlock), 0, s, AffineF<ACT>{scale, bias},
-                           x, y, n / 4, tpr);
+                           x, y, m, n / 4, tpr);
     } else {
         hipLaunchKernelGGL(k_affine_fwd_scalar<ACT>, dim3(stream_grid((m * n + 3) / 4)), dim3(kBlock), 0,
                            s, x, scale, bias, y, m, n);

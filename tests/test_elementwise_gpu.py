@@ -48,7 +48,8 @@ def test_binary_in_place(hip, orc):
 
 @pytest.mark.parametrize("op", [OP_ADD, OP_SUB, OP_MUL, OP_DIV])
 @pytest.mark.parametrize("mode", ["row", "col"])
-@pytest.mark.parametrize("m,n,off", [(512, 1024, 0), (37, 64, 0), (5, 37, 0), (3, 8, 1), (1, 1, 0)])
+@pytest.mark.parametrize("m,n,off", [(512, 1024, 0), (37, 64, 0), (6, 280, 0), (13, 1028, 0), (5, 37, 0), (3, 8, 1),
+                                     (1, 1, 0)])
 def test_broadcast(hip, orc, op, mode, m, n, off):
     x = SplitMix64(m * 7 + n).normal((m, n), 0.0, 2.0)
     y = SplitMix64(m + n * 3).uniform((n if mode == "row" else m,), 0.5, 1.5)
@@ -156,6 +157,18 @@ def test_affine_small(hip, orc, c3_small, act, off):
     y = affine_fwd_gpu(x, s, b, act, off)
     check_fwd(x, s, b, act, y, orc)
     check_bwd(x, s, y, g, act, affine_bwd_gpu(x, s, y, g, act), orc)
+
+
+@pytest.mark.parametrize("act", [ACT_RELU, ACT_SIGMOID, ACT_TANH])
+@pytest.mark.parametrize("m,n", [(7, 264), (1, 4), (5, 2056)])
+def test_affine_ragged(hip, orc, act, m, n):
+    """Row counts off a multiple of four and rows of 66, 1 and 514 float4
+    (a partial last 64-float4 column tile) on the vector path."""
+    g = SplitMix64(0xA5 + m + n)
+    x, s, b, dy = g.normal((m, n)), g.uniform((n,), 0.5, 1.5), g.normal((n,), 0.0, 0.1), g.normal((m, n))
+    y = affine_fwd_gpu(x, s, b, act)
+    check_fwd(x, s, b, act, y, orc)
+    check_bwd(x, s, y, dy, act, affine_bwd_gpu(x, s, y, dy, act), orc)
 
 
 @pytest.mark.parametrize("act", [ACT_RELU, ACT_SIGMOID, ACT_TANH])
