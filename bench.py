@@ -253,7 +253,9 @@ def wl_g16(E, D):
     for name, dt, m, k, n in shapes:
         a, b, c = rand16((m, k), dt), rand16((k, n), dt), D((m, n), np.uint16)
         keep += [a, b, c]
-        kern = "k_gemm16_ring+k_t16" if m % 256 == 0 and n % 256 == 0 and (m // 256) * (n // 256) >= 128 else "k_gemm16"
+        # the automatic choice for these NN shapes: the 256 ring at >= 128
+        # tiles of 256x256, else the 128 ring (B read as stored by both)
+        kern = "k_gemm16_ring<256>" if (m // 256) * (n // 256) >= 128 else "k_gemm16_ring<128>"
         ops.append(Op(name, kern, lambda i, a=a, b=b, c=c, m=m, k=k, n=n, dt=dt: E.matrix_t.matmul_t(a, b, c, m, k, n, dt),
                       2 * m * n * k, unit="FLOP", peak=PEAK_BF16_TFLOPS))
     desc = {"workload": "bf16/fp16 matmul NN (8192^3 bf16 and fp16, 4096^3 and 4096x1024x1024 bf16)",

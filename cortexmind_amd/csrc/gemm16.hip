@@ -9,14 +9,15 @@
 // accurate of the two; results differ from the exact product of the 16-bit
 // inputs by the fp32 accumulation error plus the final rounding.
 //
-// Three kernels, chosen by shape (gemm16() below), all accumulating each
+// Four kernels, chosen by shape (gemm16() below), all accumulating each
 // output over k in the same order (32x32x16 blocks in k order), so they
 // give the same bits:
-//  * k_gemm16_ring: 256x256 tiles, four LDS stages filled by direct
-//    global-to-LDS loads; for M, N multiples of 256 and K of 128 (operands
-//    not stored k-contiguous are transposed into the workspace first);
+//  * k_gemm16_ring<TM = 256 or 128>: TMxTM tiles, four LDS stages filled by
+//    direct global-to-LDS loads, for M, N multiples of TM and K of 128; B
+//    is read as stored ([K,N] through the LDS transpose reads of gfx950,
+//    or B^T [N,K]), A stored [K,M] is transposed into the workspace first;
 //  * k_gemm16_big: 256x256 tiles with register staging, any shape;
-//  * k_gemm16: 128x128 tiles, for grids too small for 256x256 tiles.
+//  * k_gemm16: 128x128 tiles with register staging, any shape.
 // MFMA operand layout (32x32x16): lane l supplies A[l%32][8*(l/32) .. +7]
 // and B[8*(l/32) .. +7][l%32]; accumulator register r of lane l holds
 // C[8*(r/4) + 4*(l/32) + r%4][l%32].
@@ -529,39 +530,63 @@ __global__ __launch_bounds__(kHThreads) void k_gemm16_big(const uint16_t *__rest
         }
 }
 
-// ----------------------------------------- NT ring: four LDS stages of BK 32
+// ----------------------------------------------- ring: four LDS stages of BK 32
 //
-// Both operands k-contiguous (A [M,K], B stored as B^T [N,K]), interior
-// tiles only (M, N multiples of 256, K a multiple of 128).  A 256x256
-// workgroup tile, four waves of 128x128 as above, but the k loop runs over
-// a ring of four LDS stages of 32 k (16 KB per operand per stage) filled
-// by global_load_lds_dwordx4 three steps ahead.  Each stage is its own
-// __shared__ array and the loop is unrolled over the ring, so the compiler
-// can tell a stage being read from the stages being filled and does not
-// wait for every outstanding LDS load before each fragment read.
-// A step: MFMAs of k block 0 (the next block's fragments read between
-// them); wait for the next stage's loads and the barrier; issue the loads
-// of the stage freed by the previous step; MFMAs of k block 1 with the next
-// stage's block-0 fragments read between them.
-// Rows of 64 bytes, the four 16-byte groups of row r XOR-keyed by
-// (r / 4) % 4: 16 consecutive rows, one group each, land on 16 distinct
-// 16-byte slots of the 64 banks.
+// A TM x TM workgroup tile (TM = 256 or 128), four waves of TM/2 x TM/2
+// (NB x NB MFMA blocks of 32x32, NB = TM/64), interior tiles only (M, N
+// multiples of TM, K a multiple of 128).  The k loop runs over a ring of
+// four LDS stages of 32 k, filled by global_load_lds_dwordx4 four steps
+// ahead (three tiles in flight).  Each stage is its own __shared__ array
+// and the loop is unrolled over the ring, so the compiler can tell a stage
+// being read from the stages being filled and does not wait for every
+// outstanding LDS load before each fragment read.
+// A step on stage t: MFMAs of k block 0 with block 1's fragments read
+// between them; the ring barrier (this wave's loads of stage t+1 landed,
+// every wave done reading stage t); the next stage's block-0 fragments;
+// loads of tile t+4 into stage t; MFMAs of k block 1.
+//
+// A is stored [M,K] (k contiguous).  Its stage holds TM rows of 64 bytes,
+// the four 16-byte groups of row r XOR-keyed by (r / 4) % 4: 16
+// consecutive rows, one group each, land on 16 distinct 16-byte slots of
+// the 64 banks, so a ds_read_b128 fragment read is conflict-free.
+// B is either stored as B^T [N,K] (KB, same stage layout as A) or as
+// [K,N] (n contiguous).  The [K,N] stage holds 32 k rows of TM columns as
+// loaded, 16-byte chunk c of row r at c ^ 4*(r % 4), and fragments come
+// from ds_read_b64_tr_b16: in each 16-lane group, result lane i element e
+// is element i % 4 of the 64 bits addressed by lane i / 4 + 4 e.  Lane j
+// of a group addresses row k0 + j / 4, columns n0 + 4 (j % 4) .. +3, so
+// lane i receives B[k0 .. k0+3][n0 + i]: four consecutive k of one column,
+// half of a 32x32x16 operand; two reads give the eight.  The chunk key puts
+// the four rows one read touches (64 bytes each) on distinct banks.
 constexpr int kR_BK = 32;
-constexpr int kR_TILE = 256 * kR_BK;  // elements per operand stage
+
+template <int TM>
+struct Ring {
+    static constexpr int NB = TM / 64;            // 32x32 blocks per wave side
+    static constexpr int TILE = TM * kR_BK;       // elements per operand stage
+    static constexpr int ISSUES = TM / 64;        // load instructions per wave per operand per stage
+    static constexpr int PER_STAGE = 2 * ISSUES;  // loads a wave has in flight per stage
+};
 
 __device__ __forceinline__ int rkey(int r) { return (r >> 2) & 3; }
 __device__ __forceinline__ int roff(int row, int g) { return row * kR_BK + 8 * (g ^ rkey(row)); }
+// element offset of (k row r, column n) in a [K,N] stage of TM columns
+template <int TM>
+__device__ __forceinline__ int noff(int r, int n) {
+    return r * TM + ((((n >> 3) ^ (4 * (r & 3)))) << 3) + (n & 7);
+}
 
-// Loads one 256 x 32 stage of X (k-contiguous, row stride Kd) at rows r0..,
-// k0..: each wave fills 64 rows, 16 per instruction (lane L: row L/4, LDS
+// Loads one TM x 32 stage of X (k-contiguous, row stride Kd) at rows r0..,
+// k0..: each wave fills TM/4 rows, 16 per instruction (lane L: row L/4, LDS
 // group L%4, global group (L%4) ^ key).
+template <int TM>
 __device__ __forceinline__ void ring_issue(const uint16_t *__restrict__ X, size_t r0, size_t k0, size_t Kd,
                                            uint16_t *stage) {
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
     const int rr = lane >> 2, p = lane & 3;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const int rb = w * 64 + s * 16;
+    for (int s = 0; s < Ring<TM>::ISSUES; ++s) {
+        const int rb = w * (TM / 4) + s * 16;
         const int row = rb + rr;
         const uint16_t *src = X + (r0 + row) * Kd + k0 + 8 * (p ^ rkey(row));
         __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(stage + rb * kR_BK), 16, 0,
@@ -569,60 +594,143 @@ __device__ __forceinline__ void ring_issue(const uint16_t *__restrict__ X, size_
     }
 }
 
-template <int DT>
+// Loads one 32 x TM stage of B stored [K,N] (row stride N) at k rows k0..,
+// columns n0..: each wave fills 8 rows; an instruction covers 1 KiB, i.e.
+// 64 / (TM/8) rows (lane L: row L / (TM/8), LDS chunk L % (TM/8), global
+// chunk (L % (TM/8)) ^ 4*(row % 4)).
+template <int TM>
+__device__ __forceinline__ void ring_issue_n(const uint16_t *__restrict__ B, size_t k0, size_t n0, size_t N,
+                                             uint16_t *stage) {
+    constexpr int CPR = TM / 8;      // 16-byte chunks per row
+    constexpr int RPI = kWave / CPR;  // rows per instruction
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const int rr = lane / CPR, p = lane % CPR;
+#pragma unroll
+    for (int s = 0; s < Ring<TM>::ISSUES; ++s) {
+        const int rb = w * 8 + s * RPI;
+        const int row = rb + rr;
+        const uint16_t *src = B + (k0 + row) * N + n0 + 8 * (p ^ (4 * (row & 3)));
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(stage + rb * TM), 16, 0, 0);
+    }
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// Fragments of k block kb (16 k) of a stage: A rows wm*TM/2 + 32 i + l32,
+// eight k at 16 kb + 8 lhi; B likewise from the k-contiguous or the [K,N]
+// stage.
+template <int TM, bool KB>
 __device__ __forceinline__ void ring_frags(const uint16_t *sa, const uint16_t *sb, int kb, int wm, int wn, int l32,
-                                           int lhi, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
+                                           int lhi, u32x4 (&fa)[Ring<TM>::NB], u32x4 (&fb)[Ring<TM>::NB]) {
+    constexpr int NB = Ring<TM>::NB;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        fa[i] = *reinterpret_cast<const u32x4 *>(sa + roff(wm * 128 + i * 32 + l32, 2 * kb + lhi));
+    for (int i = 0; i < NB; ++i)
+        fa[i] = *reinterpret_cast<const u32x4 *>(sa + roff(wm * (TM / 2) + i * 32 + l32, 2 * kb + lhi));
+    if constexpr (KB) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        fb[j] = *reinterpret_cast<const u32x4 *>(sb + roff(wn * 128 + j * 32 + l32, 2 * kb + lhi));
+        for (int j = 0; j < NB; ++j)
+            fb[j] = *reinterpret_cast<const u32x4 *>(sb + roff(wn * (TM / 2) + j * 32 + l32, 2 * kb + lhi));
+    } else {
+        const int lane = threadIdx.x & (kWave - 1);
+        const int g = lane >> 4, jj = lane & 15;
+        const int r = 16 * kb + 8 * (g >> 1) + (jj >> 2);
+        const int c = 16 * (g & 1) + 4 * (jj & 3);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int n = wn * (TM / 2) + j * 32 + c;
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4 *)(sb + noff<TM>(r, n)));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4 *)(sb + noff<TM>(r + 4, n)));
+            const u32x2 ul = __builtin_bit_cast(u32x2, lo), uh = __builtin_bit_cast(u32x2, hi);
+            fb[j] = u32x4{ul.x, ul.y, uh.x, uh.y};
+        }
+    }
 }
 
-template <int DT>
-__device__ __forceinline__ void ring_mfma(const u32x4 (&fa)[4], const u32x4 (&fb)[4], f32x16 (&acc)[4][4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<DT>(fa[i], fb[j], acc[i][j]);
+// The ring's barrier: this wave waits until at most PENDING of its
+// global_load_lds are outstanding (loads retire in order, so every older
+// fill has landed in LDS) and for its own LDS reads, then joins the
+// workgroup barrier; after it, every wave's older fills are visible and
+// every wave's reads of the stage about to be refilled are done.  Not
+// __syncthreads(): its workgroup-scope fence makes the compiler wait for
+// all outstanding global_load_lds (vmcnt(0)), the fills the ring means to
+// keep in flight included.  The memory clobber keeps the compiler from
+// moving LDS accesses across it.
+template <int PENDING>
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(PENDING) : "memory");
 }
 
-// Step t on stage (sa, sb); (na_s, nb_s) is stage t+1; (fa_s, fb_s) is the
-// stage freed by step t-1, refilled here with tile t+3 (tile kf).
-template <int DT>
+template <int DT, int NB>
+__device__ __forceinline__ void ring_mfma(const u32x4 (&fa)[NB], const u32x4 (&fb)[NB], f32x16 (&acc)[NB][NB]) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[i][j] = mfma16<DT>(fa[i], fb[j], acc[i][j]);
+}
+
+// Interleaves a k block's MFMAs with the fragment reads of the next block:
+// two MFMAs per read for the 256 tile with k-contiguous B (eight reads),
+// otherwise one MFMA per read until either runs out.
+template <int TM, bool KB>
+__device__ __forceinline__ void ring_interleave() {
+    constexpr int NM = Ring<TM>::NB * Ring<TM>::NB;
+    constexpr int ND = Ring<TM>::NB * (KB ? 2 : 3);
+    if constexpr (TM == 256 && KB) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+    } else {
+        constexpr int P = NM < ND ? NM : ND;
+#pragma unroll
+        for (int t = 0; t < P; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if constexpr (NM > P) __builtin_amdgcn_sched_group_barrier(0x008, NM - P, 0);
+        if constexpr (ND > P) __builtin_amdgcn_sched_group_barrier(0x100, ND - P, 0);
+    }
+}
+
+// Fills a B stage: k-contiguous (B^T [N,K], rows n0..) or [K,N] (k rows k0..).
+template <int TM, bool KB>
+__device__ __forceinline__ void ring_issue_b(const uint16_t *__restrict__ B, size_t n0, size_t kf, size_t K, size_t N,
+                                             uint16_t *stage) {
+    if constexpr (KB) ring_issue<TM>(B, n0, kf, K, stage);
+    else ring_issue_n<TM>(B, kf, n0, N, stage);
+}
+
+// Step t on stage cur (A tile at +0, B tile at +TILE, tile t); nxt holds
+// tile t+1.  After the barrier every wave has read all of cur, which is
+// refilled at once with tile t+4 (k offset kf): three tiles stay in flight.
+template <int DT, int TM, bool KB>
 __device__ __forceinline__ void ring_step(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B, size_t K,
-                                          size_t m0, size_t n0, size_t kf, const uint16_t *sa, const uint16_t *sb,
-                                          const uint16_t *na_s, const uint16_t *nb_s, uint16_t *fill_a,
-                                          uint16_t *fill_b, u32x4 (&fa)[4], u32x4 (&fb)[4], f32x16 (&acc)[4][4],
-                                          int wm, int wn, int l32, int lhi) {
-    u32x4 ga[4], gb[4];
-    ring_frags<DT>(sa, sb, 1, wm, wn, l32, lhi, ga, gb);  // block 1, during block 0's MFMAs
-    ring_mfma<DT>(fa, fb, acc);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    // the next stage has landed (only the most recent fill may be in flight)
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    __syncthreads();
-    ring_issue(A, m0, kf, K, fill_a);
-    ring_issue(B, n0, kf, K, fill_b);
-    ring_frags<DT>(na_s, nb_s, 0, wm, wn, l32, lhi, fa, fb);  // next step's block 0
-    ring_mfma<DT>(ga, gb, acc);
-    __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
+                                          size_t N, size_t m0, size_t n0, size_t kf, uint16_t *cur,
+                                          const uint16_t *nxt, u32x4 (&fa)[Ring<TM>::NB], u32x4 (&fb)[Ring<TM>::NB],
+                                          f32x16 (&acc)[Ring<TM>::NB][Ring<TM>::NB], int wm, int wn, int l32,
+                                          int lhi) {
+    constexpr int NB = Ring<TM>::NB, TILE = Ring<TM>::TILE;
+    u32x4 ga[NB], gb[NB];
+    ring_frags<TM, KB>(cur, cur + TILE, 1, wm, wn, l32, lhi, ga, gb);  // block 1, during block 0's MFMAs
+    ring_mfma<DT, NB>(fa, fb, acc);
+    ring_interleave<TM, KB>();
+    ring_barrier<2 * Ring<TM>::PER_STAGE>();  // tile t+1 has landed; tiles t+2, t+3 may be in flight
+    ring_frags<TM, KB>(nxt, nxt + TILE, 0, wm, wn, l32, lhi, fa, fb);  // next step's block 0
+    ring_issue<TM>(A, m0, kf, K, cur);
+    ring_issue_b<TM, KB>(B, n0, kf, K, N, cur + TILE);
+    ring_mfma<DT, NB>(ga, gb, acc);
+    ring_interleave<TM, KB>();
+    __builtin_amdgcn_sched_group_barrier(0x020, Ring<TM>::PER_STAGE, 0);
 }
 
 // Tile order: the XCD remap gives each XCD a contiguous range of tile ids;
 // inside it, ids walk down GM tile rows before moving one tile column, so
-// the ~32 tiles an XCD runs at once share GM row blocks of A and 32/GM
-// column blocks of B in its L2 (one tile row would share 1 and 32).
+// the tiles an XCD runs at once share GM row blocks of A and a few column
+// blocks of B in its L2 (one tile row would share 1 and all of them).
 __device__ __forceinline__ void group_tile(unsigned id, unsigned tiles_m, unsigned tiles_n, unsigned gm, unsigned *tm,
                                            unsigned *tn) {
     const unsigned per_group = gm * tiles_n;
@@ -634,60 +742,78 @@ __device__ __forceinline__ void group_tile(unsigned id, unsigned tiles_m, unsign
     *tn = in / rows;
 }
 
-template <int DT>
+// C = A B with A [M,K]; B as B^T [N,K] (KB) or [K,N].
+template <int DT, int TM, bool KB>
 __global__ __launch_bounds__(kHThreads) void k_gemm16_ring(const uint16_t *__restrict__ A,
                                                            const uint16_t *__restrict__ B, uint16_t *__restrict__ C,
                                                            size_t M, size_t N, size_t K, unsigned tiles_n,
                                                            unsigned gm) {
-    __shared__ __attribute__((aligned(16))) uint16_t a0[kR_TILE], a1[kR_TILE], a2[kR_TILE], a3[kR_TILE];
-    __shared__ __attribute__((aligned(16))) uint16_t b0[kR_TILE], b1[kR_TILE], b2[kR_TILE], b3[kR_TILE];
+    constexpr int NB = Ring<TM>::NB, TILE = Ring<TM>::TILE, PS = Ring<TM>::PER_STAGE;
+    // one array per stage (A tile, then B tile), so the compiler's tracking
+    // of outstanding loads into LDS tells the four stages apart
+    __shared__ __attribute__((aligned(16))) uint16_t s0[2 * TILE], s1[2 * TILE], s2[2 * TILE], s3[2 * TILE];
     unsigned tm, tn;
-    group_tile(xcd_remap16(blockIdx.x, gridDim.x), static_cast<unsigned>(M / kG_BM), tiles_n, gm, &tm, &tn);
-    const size_t m0 = static_cast<size_t>(tm) * kG_BM;
-    const size_t n0 = static_cast<size_t>(tn) * kG_BN;
+    group_tile(xcd_remap16(blockIdx.x, gridDim.x), static_cast<unsigned>(M / TM), tiles_n, gm, &tm, &tn);
+    const size_t m0 = static_cast<size_t>(tm) * TM;
+    const size_t n0 = static_cast<size_t>(tn) * TM;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int wm = wave >> 1, wn = wave & 1;
     const int l32 = lane & 31, lhi = lane >> 5;
 
-    f32x16 acc[4][4];
+    f32x16 acc[NB][NB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NB; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NB; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     // K % 128 == 0: tiles 0..T-1, T >= 4.  Tiles beyond T-1 reload tile T-1
-    // into a stage that is never read again.
+    // into stages whose fragments are not used.
     const size_t T = K / kR_BK;
     auto kt = [&](size_t t) { return (t < T ? t : T - 1) * kR_BK; };
-    ring_issue(A, m0, kt(0), K, a0);
-    ring_issue(B, n0, kt(0), K, b0);
-    ring_issue(A, m0, kt(1), K, a1);
-    ring_issue(B, n0, kt(1), K, b1);
-    ring_issue(A, m0, kt(2), K, a2);
-    ring_issue(B, n0, kt(2), K, b2);
-    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    __syncthreads();
-    u32x4 fa[4], fb[4];
-    ring_frags<DT>(a0, b0, 0, wm, wn, l32, lhi, fa, fb);
-    for (size_t t = 0; t < T; t += 4) {
-        ring_step<DT>(A, B, K, m0, n0, kt(t + 3), a0, b0, a1, b1, a3, b3, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT>(A, B, K, m0, n0, kt(t + 4), a1, b1, a2, b2, a0, b0, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT>(A, B, K, m0, n0, kt(t + 5), a2, b2, a3, b3, a1, b1, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT>(A, B, K, m0, n0, kt(t + 6), a3, b3, a0, b0, a2, b2, fa, fb, acc, wm, wn, l32, lhi);
+    ring_issue<TM>(A, m0, kt(0), K, s0);
+    ring_issue_b<TM, KB>(B, n0, kt(0), K, N, s0 + TILE);
+    ring_issue<TM>(A, m0, kt(1), K, s1);
+    ring_issue_b<TM, KB>(B, n0, kt(1), K, N, s1 + TILE);
+    ring_issue<TM>(A, m0, kt(2), K, s2);
+    ring_issue_b<TM, KB>(B, n0, kt(2), K, N, s2 + TILE);
+    ring_issue<TM>(A, m0, kt(3), K, s3);
+    ring_issue_b<TM, KB>(B, n0, kt(3), K, N, s3 + TILE);
+    ring_barrier<3 * PS>();
+    u32x4 fa[NB], fb[NB];
+    ring_frags<TM, KB>(s0, s0 + TILE, 0, wm, wn, l32, lhi, fa, fb);
+    // eight steps per trip: the compiler's wait before the stage-0 fragment
+    // reads at the end of a trip (it loses track of which stage the loads
+    // in flight fill across the back edge) then comes once per eight steps
+    size_t t = 0;
+    for (; t + 8 <= T; t += 8) {
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 4), s0, s1, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 5), s1, s2, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 6), s2, s3, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 7), s3, s0, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 8), s0, s1, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 9), s1, s2, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 10), s2, s3, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 11), s3, s0, fa, fb, acc, wm, wn, l32, lhi);
+    }
+    if (t < T) {  // T % 8 == 4
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 4), s0, s1, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 5), s1, s2, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 6), s2, s3, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 7), s3, s0, fa, fb, acc, wm, wn, l32, lhi);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
 
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NB; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const size_t col = n0 + wn * 128 + j * 32 + l32;
+        for (int j = 0; j < NB; ++j) {
+            const size_t col = n0 + wn * (TM / 2) + j * 32 + l32;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const size_t row = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * lhi + (r % 4);
+                const size_t row = m0 + wm * (TM / 2) + i * 32 + 8 * (r / 4) + 4 * lhi + (r % 4);
                 C[row * N + col] = H<DT>::store(acc[i][j][r]);
             }
         }
@@ -778,18 +904,42 @@ int dispatch16(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size
                                   static_cast<unsigned>(tn), s);
 }
 
-// Kernel choice:
-//  * at least 128 tiles of 256x256, M and N multiples of 256, K of 128,
-//    16-byte aligned: the NT ring (operands not already k-contiguous are
-//    first transposed into the stream's workspace: 2*2*K*N bytes of
-//    traffic for B of NN, a few percent of the product's time);
-//  * at least 128 tiles of 256x256 otherwise: the 256x256 register-staged
-//    kernel (any shape);
-//  * smaller grids: 128x128 tiles (four times the workgroups).
-// g_gemm16_kernel (tests) forces 0 = 128x128, 1 = 256x256, 2 = ring where
-// the ring's shape conditions hold.
+// Kernel choice, where the ring's conditions hold (M, N multiples of the
+// tile, K of 128, 16-byte aligned bases; A stored [K,M] is first transposed
+// into the stream's workspace, B is read as stored):
+//  * at least 128 tiles of 256x256: the 256 ring, else the 256x256
+//    register-staged kernel (any shape);
+//  * smaller grids: the 128 ring, else the 128x128 register-staged kernel.
+// g_gemm16_kernel (tests) forces 0 = 128x128 staged, 1 = 256x256 staged,
+// 2 = 256 ring, 3 = 128 ring; a ring whose conditions fail falls back to
+// the staged kernel of its tile size.
 int g_gemm16_kernel = -1;
 constexpr unsigned kRingGroup = 4;
+
+template <int DT, int TM>
+int launch_ring(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size_t N, size_t K, bool ta, bool tb,
+                cxm_stream_t st) {
+    hipStream_t s = hs(st);
+    const uint16_t *Ak = A;
+    if (ta) {  // A stored [K, M]
+        Workspace ws;
+        const int rc = get_workspace(st, 0, M * K * sizeof(uint16_t), &ws);
+        if (rc) return rc;
+        uint16_t *w = static_cast<uint16_t *>(ws.scratch);
+        const int r = transpose16(A, w, K, M, s);
+        if (r) return r;
+        Ak = w;
+    }
+    const unsigned tn = static_cast<unsigned>(N / TM);
+    const dim3 grid(static_cast<unsigned>((M / TM) * (N / TM)));
+    if (tb)
+        hipLaunchKernelGGL((k_gemm16_ring<DT, TM, true>), grid, dim3(kHThreads), 0, s, Ak, B, C, M, N, K, tn,
+                           kRingGroup);
+    else
+        hipLaunchKernelGGL((k_gemm16_ring<DT, TM, false>), grid, dim3(kHThreads), 0, s, Ak, B, C, M, N, K, tn,
+                           kRingGroup);
+    return launch_status();
+}
 
 template <int DT>
 int gemm16(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size_t K, size_t N, bool ta, bool tb,
@@ -801,36 +951,17 @@ int gemm16(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size_t K
     const bool vb = aligned16(B) && (tb ? K % 8 == 0 : N % 8 == 0);
     hipStream_t s = hs(st);
     const size_t big_tiles = ((M + kG_BM - 1) / kG_BM) * ((N + kG_BN - 1) / kG_BN);
-    const bool ring_ok = M % kG_BM == 0 && N % kG_BN == 0 && K % (4 * kR_BK) == 0 && aligned16(A) && aligned16(B) &&
-                         aligned16(C);
-    int kernel = big_tiles >= 128 ? (ring_ok ? 2 : 1) : 0;
-    if (g_gemm16_kernel >= 0) kernel = g_gemm16_kernel == 2 && !ring_ok ? 1 : g_gemm16_kernel;
-    if (kernel == 2) {
-        // A as [M,K] and B as B^T [N,K], transposing into the workspace where needed
-        const size_t ta_n = ta ? M * K : 0, tb_n = tb ? 0 : K * N;
-        const uint16_t *Ak = A, *Bk = B;
-        if (ta_n + tb_n) {
-            Workspace ws;
-            const int rc = get_workspace(st, 0, (ta_n + tb_n) * sizeof(uint16_t), &ws);
-            if (rc) return rc;
-            uint16_t *w = static_cast<uint16_t *>(ws.scratch);
-            if (ta) {  // A stored [K, M]
-                const int r = transpose16(A, w, K, M, s);
-                if (r) return r;
-                Ak = w;
-            }
-            if (!tb) {  // B stored [K, N]
-                uint16_t *wb = w + ta_n;
-                const int r = transpose16(B, wb, K, N, s);
-                if (r) return r;
-                Bk = wb;
-            }
-        }
-        const unsigned tn = static_cast<unsigned>(N / kG_BN);
-        hipLaunchKernelGGL(k_gemm16_ring<DT>, dim3(static_cast<unsigned>(big_tiles)), dim3(kHThreads), 0, s, Ak, Bk,
-                           C, M, N, K, tn, kRingGroup);
-        return launch_status();
+    const bool al = aligned16(A) && aligned16(B) && aligned16(C) && K % (4 * kR_BK) == 0;
+    const bool ring256 = al && M % 256 == 0 && N % 256 == 0;
+    const bool ring128 = al && M % 128 == 0 && N % 128 == 0;
+    int kernel = big_tiles >= 128 ? (ring256 ? 2 : 1) : (ring128 ? 3 : 0);
+    if (g_gemm16_kernel >= 0) {
+        kernel = g_gemm16_kernel;
+        if (kernel == 2 && !ring256) kernel = 1;
+        if (kernel == 3 && !ring128) kernel = 0;
     }
+    if (kernel == 2) return launch_ring<DT, 256>(A, B, C, M, N, K, ta, tb, st);
+    if (kernel == 3) return launch_ring<DT, 128>(A, B, C, M, N, K, ta, tb, st);
     if (!ta && !tb) return dispatch16<DT, false, false>(A, B, C, M, N, K, va, vb, s, kernel);
     if (ta && !tb) return dispatch16<DT, true, false>(A, B, C, M, N, K, va, vb, s, kernel);
     if (!ta && tb) return dispatch16<DT, false, true>(A, B, C, M, N, K, va, vb, s, kernel);
@@ -864,7 +995,7 @@ int cxm_matmul_t(const void *a, const void *b, void *c, size_t xN, size_t yN, si
 }
 
 int cxm_gemm16_kernel(int kernel) {
-    if (kernel < -1 || kernel > 2) return CXM_E_INVALID;
+    if (kernel < -1 || kernel > 3) return CXM_E_INVALID;
     cxm::g_gemm16_kernel = kernel;
     return CXM_OK;
 }

@@ -327,10 +327,11 @@ int cxm_matmul_t(const void *a, const void *b, void *c, size_t xN, size_t yN, si
 int cxm_gemm_t(const void *a, const void *b, void *c, size_t m, size_t k, size_t n, int trans_a,
                int trans_b, int dtype, cxm_stream_t s);
 /* Kernel choice of the 16-bit GEMM, process-wide: -1 automatic (default),
- * 0 the 128x128-tile kernel, 1 the 256x256-tile kernel, 2 the 256x256
- * four-stage direct-to-LDS kernel where its shape conditions hold (M, N
- * multiples of 256, K of 128, 16-byte aligned; else 1).  All give the same
- * bits.  For tests and tuning; no reference counterpart. */
+ * 0 the 128x128-tile register-staged kernel, 1 the 256x256-tile one, 2 the
+ * 256x256 four-stage direct-to-LDS kernel, 3 the 128x128 one; 2 and 3 need
+ * M, N multiples of their tile, K of 128 and 16-byte aligned bases, else
+ * 1 and 0 run.  All give the same bits.  For tests and tuning; no
+ * reference counterpart. */
 int cxm_gemm16_kernel(int kernel);
 
 /* ----------------------------------------------------------- training step

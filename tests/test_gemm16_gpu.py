@@ -134,32 +134,49 @@ def _kernel(k):
 
 @pytest.mark.parametrize("dt", DTS, ids=["bf16", "f16"])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
-def test_kernels_agree_bitwise(hip, orc, dt, ta, tb):
-    """The 128x128, 256x256 and four-stage direct-to-LDS kernels accumulate
-    each output over k in the same order (32x32x16 MFMA blocks in k
-    order), so they give the same bits; the shape meets the direct-load
-    kernel's conditions (M, N multiples of 256, K of 128), and NN/TN/TT
-    pass through the 16-bit transpose first."""
-    m, k, n = 512, 384, 768
-    g = SplitMix64(77 + 4 * ta + 2 * tb + dt)
+@pytest.mark.parametrize("shape", [(512, 384, 768), (512, 128, 256), (256, 1024, 384)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_kernels_agree_bitwise(hip, orc, dt, ta, tb, shape):
+    """The 128x128 and 256x256 register-staged kernels and the 256 and 128
+    four-stage direct-to-LDS kernels accumulate each output over k in the
+    same order (32x32x16 MFMA blocks in k order), so they give the same
+    bits.  K of 384, 128 and 1024 take the ring's eight-step loop zero,
+    one and four times with and without its four-step tail; B stored
+    [K,N] (tb = 0) goes through the transpose reads, A stored [K,M]
+    (ta = 1) through the 16-bit transpose first.  N = 384 is not a
+    multiple of 256, so kernel 2 falls back to kernel 1 there."""
+    m, k, n = shape
+    g = SplitMix64(77 + 4 * ta + 2 * tb + dt + k)
     a16, a64 = rand16(g, (k, m) if ta else (m, k), dt, orc)
     b16, b64 = rand16(g, (n, k) if tb else (k, n), dt, orc)
     outs = []
     try:
-        for kern in (0, 1, 2):
+        for kern in (0, 1, 2, 3):
             _kernel(kern)
             outs.append(run(a16, b16, m, k, n, dt, ta, tb))
     finally:
         _kernel(-1)
     check(outs[0], a64.T if ta else a64, b64.T if tb else b64, dt, orc)
-    assert np.array_equal(outs[0], outs[1])
-    assert np.array_equal(outs[0], outs[2])
+    for o in outs[1:]:
+        assert np.array_equal(outs[0], o)
+
+
+@pytest.mark.parametrize("dt", DTS, ids=["bf16", "f16"])
+@pytest.mark.parametrize("tb", [0, 1])
+def test_ring128_default_path(hip, orc, dt, tb):
+    """4096 x 1024 x 1024: 64 tiles of 256x256, too few for the chip, so the
+    automatic choice is the 128 ring (256 workgroups), B read as stored."""
+    m, k, n = 4096, 1024, 1024
+    g = SplitMix64(6160 + dt + tb)
+    a16, a64 = rand16(g, (m, k), dt, orc)
+    b16, b64 = rand16(g, (n, k) if tb else (k, n), dt, orc)
+    check(run(a16, b16, m, k, n, dt, 0, tb), a64, b64.T if tb else b64, dt, orc)
 
 
 @pytest.mark.parametrize("dt", DTS, ids=["bf16", "f16"])
 def test_large_default_path(hip, orc, dt):
     """4096 x 1024 x 2048 NN: 128 tiles of 256x256, so the automatic choice
-    is the direct-load kernel behind a transpose of B."""
+    is the 256 direct-load kernel, B read as stored."""
     m, k, n = 4096, 1024, 2048
     g = SplitMix64(5150 + dt)
     a16, a64 = rand16(g, (m, k), dt, orc)
@@ -168,6 +185,6 @@ def test_large_default_path(hip, orc, dt):
 
 
 def test_kernel_choice_argument(hip):
-    assert lib().cxm_gemm16_kernel(3) == E_INVALID
+    assert lib().cxm_gemm16_kernel(4) == E_INVALID
     assert lib().cxm_gemm16_kernel(-2) == E_INVALID
     assert lib().cxm_gemm16_kernel(-1) == 0
