@@ -179,7 +179,7 @@ def wl_c5(E, D):
               MLP_FLOP_PER_STEP, unit="FLOP")]
     # the step's largest GEMM alone, for the MFMA roofline
     h1, w2, h2 = D((B, d1)), P["w2"], D((B, d2))
-    gemm_op = Op("gemm_fwd_4096x1024x1024", "k_gemm<NN>",
+    gemm_op = Op("gemm_fwd_4096x1024x1024", "k_gemm_ring<NN>",
                  lambda k: E.gemm(h1, w2, h2, B, d1, d2), 2 * B * d1 * d2, unit="FLOP")
     desc = {"workload": "C5 MLP 784-1024-1024-10 fp32 train step, batch 4096, SGD lr 0.01",
             "flop_per_step": MLP_FLOP_PER_STEP}

@@ -110,6 +110,7 @@ SIGNATURES = {
     "cxm_matmul_t": [_P, _P, _P, _SZ, _SZ, _SZ, _I, _P],
     "cxm_gemm_t": [_P, _P, _P, _SZ, _SZ, _SZ, _I, _I, _I, _P],
     "cxm_gemm16_kernel": [_I],
+    "cxm_gemm_f32_kernel": [_I],
     "cxm_softmax_xent_f32": [_P, _P, _P, _P, _SZ, _SZ, _P],
     "cxm_sgd_f32": [_P, _P, _F, _SZ, _P],
     "cxm_mlp3_create": [ctypes.POINTER(_P), _SZ, _SZ, _SZ, _SZ, _SZ],

@@ -131,6 +131,35 @@ __device__ __forceinline__ void st4_stream(float *p, float4 v) {
     __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4 *>(p));
 }
 
+// Direct global-to-LDS load of 16 bytes per lane (global_load_lds_dwordx4):
+// lane L's 16 bytes at gsrc land at LDS byte lds + 16 L (lds wave-uniform,
+// placed in M0).  Issued through inline asm so that the compiler's wait
+// insertion does not see an LDS write in flight: it cannot always tell which
+// LDS array such a load fills and then waits for every outstanding load
+// (vmcnt(0)) before unrelated LDS reads.  The caller orders the load against
+// LDS reads and writes itself (s_waitcnt vmcnt plus a barrier before the
+// data is read; no read of the destination in flight when it is issued) and
+// waits for it before the workgroup ends.
+__device__ __forceinline__ void lds_load16(const void *gsrc, const void *lds) {
+    const unsigned a = __builtin_amdgcn_readfirstlane(
+        static_cast<unsigned>(reinterpret_cast<size_t>((const __attribute__((address_space(3))) void *)lds)));
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gsrc), "{m0}"(a) : "memory");
+}
+
+// Barrier of an LDS ring filled by lds_load16: this wave waits until at
+// most PENDING of its global loads are outstanding (loads retire in order,
+// so every older fill has landed in LDS) and for its own LDS reads, then
+// joins the workgroup barrier; after it, every wave's older fills are
+// visible and every wave's reads of the stage about to be refilled are
+// done.  Not __syncthreads(): its workgroup-scope fence makes the compiler
+// wait for all outstanding global loads (vmcnt(0)), the fills the ring
+// means to keep in flight included.  The memory clobber keeps the compiler
+// from moving LDS accesses across it.
+template <int PENDING>
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(PENDING) : "memory");
+}
+
 // IEEE max as _mm256_max_ps(a, b): a when a > b, else b.
 __device__ __forceinline__ float vmax(float a, float b) { return a > b ? a : b; }
 

@@ -657,6 +657,169 @@ __global__ __launch_bounds__(kW4Threads) void k_gemm_w4(const float *__restrict_
     gemm_epilogue<W4I, W4J>(acc, C, M, N, m0, n0, tile, split, splits, wm, wn, lhi, l32, epi, part, counters, &flag);
 }
 
+// ------------------------------------------------ direct-to-LDS ring
+// A 256-thread workgroup (four waves of 64x64, 2x2 MFMA blocks each) per
+// 128x128 tile; K runs over a ring of four LDS stages of 32 k (16 KiB per
+// operand), filled by direct global-to-LDS loads (lds_load16) four steps
+// ahead, so three tiles are in flight while one is multiplied.  The
+// stage of step t is refilled with tile t+4 right after the ring barrier
+// that follows its last fragment read.  For M, N multiples of 128 and a K
+// range per split that is a multiple of 128.
+// Stage layouts (16-byte chunks XOR-keyed so that fragment reads are
+// conflict-free across the 64 banks):
+//  * k-contiguous operand (A [M,K], B^T [N,K]): row r of 32 floats, chunk c
+//    at c ^ ((r / 2) % 8); a fragment is one ds_read_b128 of 4 k;
+//  * the other (A^T [K,M], B [K,N]): k row of 128 floats, chunk c at
+//    c ^ 8 ((k / 4) % 2); a fragment is four ds_read_b32, lanes 0-31 on
+//    consecutive columns.
+// A 4-k fragment feeds four MFMAs: MFMA e takes k = 8 kb + e on lanes 0-31
+// and 8 kb + 4 + e on lanes 32-63 (kb the 8-k block of the stage).
+constexpr int kRingThreads = 256;
+constexpr int kRBK = 32;                    // k per stage
+constexpr int kRST = BM * kRBK;             // floats per operand stage
+constexpr int kRPS = 2 * (kRST / 4 / kRingThreads);  // lds_load16 per wave per stage (A and B)
+
+__device__ __forceinline__ int rk_c(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int rk_m(int k) { return 8 * ((k >> 2) & 1); }
+
+// Fills one operand stage: k-contiguous X[r][k] (ld = K) at rows r0..,
+// k0..: eight rows of 32 floats per instruction; else X[k][r] (ld = row
+// length) at k rows k0.., columns r0..: two k rows of 128 floats each.
+template <bool KC>
+__device__ __forceinline__ void ring_fill(const float *__restrict__ X, size_t r0, size_t k0, size_t ld, float *stage) {
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        if constexpr (KC) {
+            const int rb = w * 32 + s * 8, row = rb + (lane >> 3), p = lane & 7;
+            lds_load16(X + (r0 + row) * ld + k0 + 4 * (p ^ rk_c(row)), stage + rb * kRBK);
+        } else {
+            const int kb = w * 8 + s * 2, kr = kb + (lane >> 5), p = lane & 31;
+            lds_load16(X + (k0 + kr) * ld + r0 + 4 * (p ^ rk_m(kr)), stage + kb * BM);
+        }
+    }
+}
+
+// Fragment of 8-k block kb for tile row (or column) `row`: k = 8 kb + 4 lhi + 0..3.
+template <bool KC>
+__device__ __forceinline__ float4 ring_frag(const float *stage, int row, int kb, int lhi) {
+    if constexpr (KC) {
+        return *reinterpret_cast<const float4 *>(stage + row * kRBK + 4 * ((2 * kb + lhi) ^ rk_c(row)));
+    } else {
+        const int k = 8 * kb + 4 * lhi;
+        auto at = [&](int kk) { return stage[kk * BM + 4 * ((row >> 2) ^ rk_m(kk)) + (row & 3)]; };
+        return make_float4(at(k), at(k + 1), at(k + 2), at(k + 3));
+    }
+}
+
+struct RingFrag {
+    float4 a[2], b[2];
+};
+
+template <bool KCA, bool KCB>
+__device__ __forceinline__ void ring_frags(const float *st, int kb, int wm, int wn, int l32, int lhi, RingFrag &f) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) f.a[i] = ring_frag<KCA>(st, wm * 64 + i * 32 + l32, kb, lhi);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) f.b[j] = ring_frag<KCB>(st + kRST, wn * 64 + j * 32 + l32, kb, lhi);
+}
+
+__device__ __forceinline__ float comp(const float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
+
+// The 16 MFMAs of one 8-k block, with the next block's fragment reads
+// scheduled between them.
+template <bool KCA, bool KCB>
+__device__ __forceinline__ void ring_block(const RingFrag &f, floatx16 (&acc)[2][2]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(comp(f.a[i], e), comp(f.b[j], e), acc[i][j], 0, 0, 0);
+    constexpr int ND = (KCA ? 2 : 8) + (KCB ? 2 : 8);
+#pragma unroll
+    for (int t = 0; t < ND; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 16 - ND, 0);
+}
+
+// Step on stage cur (tile t; A at +0, B at +kRST); nxt holds tile t+1; f0
+// holds block 0 of cur on entry and block 0 of nxt on return.
+template <bool KCA, bool KCB>
+__device__ __forceinline__ void ring_step(const float *__restrict__ A, const float *__restrict__ B, size_t lda,
+                                          size_t ldb, size_t m0, size_t n0, size_t kf, float *cur, const float *nxt,
+                                          RingFrag &f0, floatx16 (&acc)[2][2], int wm, int wn, int l32, int lhi) {
+    RingFrag f1, f2;
+    ring_frags<KCA, KCB>(cur, 1, wm, wn, l32, lhi, f1);
+    ring_block<KCA, KCB>(f0, acc);
+    ring_frags<KCA, KCB>(cur, 2, wm, wn, l32, lhi, f2);
+    ring_block<KCA, KCB>(f1, acc);
+    ring_frags<KCA, KCB>(cur, 3, wm, wn, l32, lhi, f1);
+    ring_block<KCA, KCB>(f2, acc);
+    ring_barrier<2 * kRPS>();  // tile t+1 landed; every wave done reading cur
+    ring_frags<KCA, KCB>(nxt, 0, wm, wn, l32, lhi, f0);
+    ring_fill<KCA>(A, m0, kf, lda, cur);
+    ring_fill<KCB>(B, n0, kf, ldb, cur + kRST);
+    ring_block<KCA, KCB>(f1, acc);
+}
+
+// Same arguments as k_gemm.  KCA: A stored [M,K] (else [K,M]); KCB: B stored
+// [N,K] (else [K,N]).
+template <bool KCA, bool KCB>
+__global__ __launch_bounds__(kRingThreads) void k_gemm_ring(const float *__restrict__ A, const float *__restrict__ B,
+                                                            float *__restrict__ C, size_t M, size_t N, size_t K,
+                                                            unsigned tiles_n, unsigned splits, size_t kper,
+                                                            Epilogue epi, float *__restrict__ part,
+                                                            unsigned *__restrict__ counters) {
+    __shared__ __attribute__((aligned(16))) float s0[2 * kRST], s1[2 * kRST], s2[2 * kRST], s3[2 * kRST];
+    __shared__ int flag;
+    const unsigned wg = xcd_remap(blockIdx.x, gridDim.x);
+    const unsigned tile = wg / splits;
+    const unsigned split = wg - tile * splits;
+    const size_t m0 = static_cast<size_t>(tile / tiles_n) * BM;
+    const size_t n0 = static_cast<size_t>(tile % tiles_n) * BN;
+    const size_t kbeg = static_cast<size_t>(split) * kper;
+    const size_t kend = kbeg + kper < K ? kbeg + kper : K;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int wm = wave >> 1, wn = wave & 1, l32 = lane & 31, lhi = lane >> 5;
+    const size_t lda = KCA ? K : M, ldb = KCB ? K : N;
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // (kend - kbeg) % 128 == 0: tiles 0..T-1, T a multiple of 4.  Tiles
+    // beyond T-1 reload tile T-1 into stages whose fragments go unused.
+    const size_t T = (kend - kbeg) / kRBK;
+    auto kt = [&](size_t t) { return kbeg + (t < T ? t : T - 1) * kRBK; };
+    ring_fill<KCA>(A, m0, kt(0), lda, s0);
+    ring_fill<KCB>(B, n0, kt(0), ldb, s0 + kRST);
+    ring_fill<KCA>(A, m0, kt(1), lda, s1);
+    ring_fill<KCB>(B, n0, kt(1), ldb, s1 + kRST);
+    ring_fill<KCA>(A, m0, kt(2), lda, s2);
+    ring_fill<KCB>(B, n0, kt(2), ldb, s2 + kRST);
+    ring_fill<KCA>(A, m0, kt(3), lda, s3);
+    ring_fill<KCB>(B, n0, kt(3), ldb, s3 + kRST);
+    ring_barrier<3 * kRPS>();
+    RingFrag f0;
+    ring_frags<KCA, KCB>(s0, 0, wm, wn, l32, lhi, f0);
+    for (size_t t = 0; t < T; t += 4) {
+        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, kt(t + 4), s0, s1, f0, acc, wm, wn, l32, lhi);
+        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, kt(t + 5), s1, s2, f0, acc, wm, wn, l32, lhi);
+        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, kt(t + 6), s2, s3, f0, acc, wm, wn, l32, lhi);
+        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, kt(t + 7), s3, s0, f0, acc, wm, wn, l32, lhi);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
+    gemm_epilogue<2, 2>(acc, C, M, N, m0, n0, tile, split, splits, wm, wn, lhi, l32, epi, part, counters, &flag);
+}
+
 // ------------------------------------------------ skinny products
 // Products with a dimension of at most 16 (the 10-class output layer of
 // the MLP) leave a 128x128 MFMA tile almost empty; they are bandwidth
@@ -865,10 +1028,11 @@ __global__ __launch_bounds__(kThinNT) void k_gemm_thin_k(const float *__restrict
     }
 }
 
-// Kernel variant per launch.  -1 (the library's setting) chooses by shape;
-// a tuning program that compiles this file can pin one: 0 k-major, 1/2
+// Kernel variant per launch.  -1 (the default) chooses by shape;
+// cxm_gemm_f32_kernel pins one for tests and tuning: 0 k-major, 1/2
 // k-contiguous with BK 32/64, 3/4 four-wave with BK 32/64, 5 k-contiguous
-// without the XCD renumbering, 6 k-major with it.
+// without the XCD renumbering, 6 k-major with it, 7 the direct-to-LDS ring
+// (where its shape conditions hold, else 1).
 int g_gemm_kc = -1;
 
 // Measured on gfx950 (TFLOP/s, best variant vs the others):
@@ -878,8 +1042,14 @@ int g_gemm_kc = -1;
 //    renumbering (97.5 and 77 against 87-89 and 70-75);
 //  * A B and A B^T at 256-tile grids: k-contiguous tiles, BK 32, with the
 //    renumbering (93 and 104 against 90 and 94 for the k-major kernel).
-inline int gemm_variant(bool ta, bool tb, unsigned wgs) {
+//  * the ring (M, N, K multiples of 128, 16-byte aligned bases) for A B and
+//    A B^T: 99-100 against 92-95 at 4096x1024x1024, 133 against 113 at
+//    4096^3, 135 against 125 at 8192^3; A^T B (split K) measured even and
+//    keeps the k-major kernel.
+inline int gemm_variant(bool ta, bool tb, unsigned wgs, bool ring_ok) {
+    if (g_gemm_kc == 7) return ring_ok ? 7 : 1;
     if (g_gemm_kc >= 0) return g_gemm_kc;
+    if (ring_ok && !ta) return 7;
     if (wgs >= 1024) return 3;
     if (ta && !tb) return 6;
     return 1;
@@ -889,6 +1059,11 @@ template <bool TA, bool TB>
 int launch_t(const float *A, const float *B, float *C, size_t M, size_t N, size_t K, bool va, bool vb,
              dim3 grid, unsigned tiles_n, unsigned splits, size_t kper, Epilogue epi, float *part,
              unsigned *counters, hipStream_t s, int variant) {
+    if (variant == 7) {
+        hipLaunchKernelGGL((k_gemm_ring<!TA, TB>), grid, dim3(kRingThreads), 0, s, A, B, C, M, N, K, tiles_n, splits,
+                           kper, epi, part, counters);
+        return launch_status();
+    }
 #define CXM_GEMM_LAUNCH(VA_, VB_)                                                                  \
     if (variant == 5)                                                                              \
         hipLaunchKernelGGL((k_gemm_kc<TA, TB, VA_, VB_, 32, false>), grid, dim3(kGemmThreads), 0, s, A, B, C, M, N, \
@@ -984,9 +1159,11 @@ int gemm_ex(const float *A, const float *B, float *C, size_t M, size_t K, size_t
         if (splits > max_splits) splits = max_splits;
         if (splits < 1) splits = 1;
     }
-    // a split's k range is a whole number of the kernel's k steps
-    const int variant = gemm_variant(ta, tb, static_cast<unsigned>(tiles * splits));
-    const size_t kstep = (variant == 2 || variant == 4) ? 64 : BK;
+    // a split's k range is a whole number of the kernel's k steps (the
+    // ring's: four stages of 32)
+    const bool ring_ok = M % BM == 0 && N % BN == 0 && K % (4 * kRBK) == 0 && aligned16(A) && aligned16(B);
+    const int variant = gemm_variant(ta, tb, static_cast<unsigned>(tiles * splits), ring_ok);
+    const size_t kstep = variant == 7 ? 4 * kRBK : (variant == 2 || variant == 4) ? 64 : BK;
     size_t kper = (K + splits - 1) / splits;
     kper = (kper + kstep - 1) / kstep * kstep;
     splits = (K + kper - 1) / kper;
@@ -1019,6 +1196,12 @@ extern "C" {
 int cxm_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t k, size_t n, int trans_a,
                  int trans_b, const float *bias, int act, const float *gate, cxm_stream_t s) {
     return cxm::gemm_ex(a, b, c, m, k, n, trans_a != 0, trans_b != 0, cxm::Epilogue{bias, gate, act, 0, 0.0f}, s);
+}
+
+int cxm_gemm_f32_kernel(int variant) {
+    if (variant < -1 || variant > 7) return CXM_E_INVALID;
+    cxm::g_gemm_kc = variant;
+    return CXM_OK;
 }
 
 int cxm_matmul_f32(const float *a, const float *b, float *c, size_t xN, size_t yN, size_t zN,

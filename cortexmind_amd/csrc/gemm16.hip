@@ -535,11 +535,9 @@ __global__ __launch_bounds__(kHThreads) void k_gemm16_big(const uint16_t *__rest
 // A TM x TM workgroup tile (TM = 256 or 128), four waves of TM/2 x TM/2
 // (NB x NB MFMA blocks of 32x32, NB = TM/64), interior tiles only (M, N
 // multiples of TM, K a multiple of 128).  The k loop runs over a ring of
-// four LDS stages of 32 k, filled by global_load_lds_dwordx4 four steps
-// ahead (three tiles in flight).  Each stage is its own __shared__ array
-// and the loop is unrolled over the ring, so the compiler can tell a stage
-// being read from the stages being filled and does not wait for every
-// outstanding LDS load before each fragment read.
+// four LDS stages of 32 k, filled by direct global-to-LDS loads
+// (lds_load16) four steps ahead (three tiles in flight); the loop is
+// unrolled over the ring so that stage addresses are constants.
 // A step on stage t: MFMAs of k block 0 with block 1's fragments read
 // between them; the ring barrier (this wave's loads of stage t+1 landed,
 // every wave done reading stage t); the next stage's block-0 fragments;
@@ -589,8 +587,7 @@ __device__ __forceinline__ void ring_issue(const uint16_t *__restrict__ X, size_
         const int rb = w * (TM / 4) + s * 16;
         const int row = rb + rr;
         const uint16_t *src = X + (r0 + row) * Kd + k0 + 8 * (p ^ rkey(row));
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(stage + rb * kR_BK), 16, 0,
-                                         0);
+        lds_load16(src, stage + rb * kR_BK);
     }
 }
 
@@ -610,7 +607,7 @@ __device__ __forceinline__ void ring_issue_n(const uint16_t *__restrict__ B, siz
         const int rb = w * 8 + s * RPI;
         const int row = rb + rr;
         const uint16_t *src = B + (k0 + row) * N + n0 + 8 * (p ^ (4 * (row & 3)));
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(stage + rb * TM), 16, 0, 0);
+        lds_load16(src, stage + rb * TM);
     }
 }
 
@@ -647,20 +644,6 @@ __device__ __forceinline__ void ring_frags(const uint16_t *sa, const uint16_t *s
             fb[j] = u32x4{ul.x, ul.y, uh.x, uh.y};
         }
     }
-}
-
-// The ring's barrier: this wave waits until at most PENDING of its
-// global_load_lds are outstanding (loads retire in order, so every older
-// fill has landed in LDS) and for its own LDS reads, then joins the
-// workgroup barrier; after it, every wave's older fills are visible and
-// every wave's reads of the stage about to be refilled are done.  Not
-// __syncthreads(): its workgroup-scope fence makes the compiler wait for
-// all outstanding global_load_lds (vmcnt(0)), the fills the ring means to
-// keep in flight included.  The memory clobber keeps the compiler from
-// moving LDS accesses across it.
-template <int PENDING>
-__device__ __forceinline__ void ring_barrier() {
-    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(PENDING) : "memory");
 }
 
 template <int DT, int NB>
@@ -749,8 +732,7 @@ __global__ __launch_bounds__(kHThreads) void k_gemm16_ring(const uint16_t *__res
                                                            size_t M, size_t N, size_t K, unsigned tiles_n,
                                                            unsigned gm) {
     constexpr int NB = Ring<TM>::NB, TILE = Ring<TM>::TILE, PS = Ring<TM>::PER_STAGE;
-    // one array per stage (A tile, then B tile), so the compiler's tracking
-    // of outstanding loads into LDS tells the four stages apart
+    // one array per stage: A tile, then B tile
     __shared__ __attribute__((aligned(16))) uint16_t s0[2 * TILE], s1[2 * TILE], s2[2 * TILE], s3[2 * TILE];
     unsigned tm, tn;
     group_tile(xcd_remap16(blockIdx.x, gridDim.x), static_cast<unsigned>(M / TM), tiles_n, gm, &tm, &tn);
@@ -784,21 +766,7 @@ __global__ __launch_bounds__(kHThreads) void k_gemm16_ring(const uint16_t *__res
     ring_barrier<3 * PS>();
     u32x4 fa[NB], fb[NB];
     ring_frags<TM, KB>(s0, s0 + TILE, 0, wm, wn, l32, lhi, fa, fb);
-    // eight steps per trip: the compiler's wait before the stage-0 fragment
-    // reads at the end of a trip (it loses track of which stage the loads
-    // in flight fill across the back edge) then comes once per eight steps
-    size_t t = 0;
-    for (; t + 8 <= T; t += 8) {
-        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 4), s0, s1, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 5), s1, s2, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 6), s2, s3, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 7), s3, s0, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 8), s0, s1, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 9), s1, s2, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 10), s2, s3, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 11), s3, s0, fa, fb, acc, wm, wn, l32, lhi);
-    }
-    if (t < T) {  // T % 8 == 4
+    for (size_t t = 0; t < T; t += 4) {
         ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 4), s0, s1, fa, fb, acc, wm, wn, l32, lhi);
         ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 5), s1, s2, fa, fb, acc, wm, wn, l32, lhi);
         ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 6), s2, s3, fa, fb, acc, wm, wn, l32, lhi);

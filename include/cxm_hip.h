@@ -316,6 +316,13 @@ int cxm_matmul_f32(const float *a, const float *b, float *c, size_t xN, size_t y
 int cxm_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t k, size_t n,
                  int trans_a, int trans_b, const float *bias, int act, const float *gate,
                  cxm_stream_t s);
+/* Kernel choice of the fp32 GEMM, process-wide: -1 automatic (default),
+ * 0..6 the register-staged variants, 7 the four-stage direct-to-LDS ring
+ * (M, N, K multiples of 128 and 16-byte aligned bases, else variant 1).
+ * Results agree within the fp32 tolerance; the ring and variant 1 sum each
+ * output over k in the same order and give the same bits for A B and
+ * A B^T.  For tests and tuning; no reference counterpart. */
+int cxm_gemm_f32_kernel(int variant);
 /* matmul for any CXM_DT_*: nv::Matrix::matmul (Engine/CUDA/matrix.cu:112-159)
  * with its per-dtype cublasGemmEx (BlasTraits, matrix.cu:18-37).  bf16 and
  * fp16 operands and output (16-bit element arrays), fp32 accumulation on

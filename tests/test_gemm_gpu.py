@@ -84,6 +84,52 @@ def test_gemm_large_grid_float64(hip, m, k, n, ta, tb):
     assert np.all(np.abs(got - ref) <= bound(a, b) + 1e-6 * np.abs(bias)[None, :])
 
 
+def _pin(variant):
+    assert lib().cxm_gemm_f32_kernel(variant) == 0
+
+
+@pytest.mark.parametrize("m,k,n", [(128, 128, 128), (256, 384, 512), (512, 1024, 256)], ids=lambda v: str(v))
+@pytest.mark.parametrize("tb", [0, 1])
+def test_ring_same_bits_as_kc(hip, m, k, n, tb):
+    """The direct-to-LDS ring (variant 7) and the k-contiguous kernel
+    (variant 1) sum each output over k in the same order, so A B and A B^T
+    agree bitwise; both within the bound of the float64 product."""
+    g = SplitMix64(m + 5 * k + 9 * n + tb)
+    a, b = g.normal((m, k)), g.normal((k, n))
+    try:
+        _pin(7)
+        r7 = run(a, b, 0, tb)
+        _pin(1)
+        r1 = run(a, b, 0, tb)
+    finally:
+        _pin(-1)
+    assert np.array_equal(r7.view(np.uint32), r1.view(np.uint32))
+    assert np.all(np.abs(r7 - a.astype(np.float64) @ b.astype(np.float64)) <= bound(a, b))
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 4096, 256), (384, 512, 640)], ids=lambda v: str(v))
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_ring_all_forms_float64(hip, m, k, n, ta, tb):
+    """Variant 7 pinned for every stored form with the bias + ReLU epilogue;
+    256 x 4096 x 256 has 4 tiles and splits K 16 ways (256 each)."""
+    g = SplitMix64(31 * m + k + 7 * n + 3 * ta + tb)
+    a, b = g.normal((m, k)), g.normal((k, n))
+    bias = g.normal((n,), 0.0, 0.5)
+    try:
+        _pin(7)
+        got = run(a, b, ta, tb, bias=bias, act=ACT_RELU)
+    finally:
+        _pin(-1)
+    ref = np.maximum(a.astype(np.float64) @ b.astype(np.float64) + bias.astype(np.float64), 0.0)
+    assert np.all(np.abs(got - ref) <= bound(a, b) + 1e-6 * np.abs(bias)[None, :])
+
+
+def test_kernel_pin_argument(hip):
+    assert lib().cxm_gemm_f32_kernel(8) == E_INVALID
+    assert lib().cxm_gemm_f32_kernel(-2) == E_INVALID
+    assert lib().cxm_gemm_f32_kernel(-1) == 0
+
+
 def test_epilogue_bias_relu_gate(hip, orc):
     g = SplitMix64(17)
     a, b = g.normal((200, 96)), g.normal((96, 72))
