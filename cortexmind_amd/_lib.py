@@ -105,6 +105,7 @@ SIGNATURES = {
     "cxm_softmax_fwd_f32": [_P, _P, _SZ, _SZ, _I, _P],
     "cxm_softmax_bwd_f32": [_P, _P, _P, _SZ, _SZ, _I, _P],
     "cxm_exchange_wait_limit": [ctypes.c_uint, _P],
+    "cxm_softmax_stagger": [_I, _P],
     "cxm_matmul_f32": [_P, _P, _P, _SZ, _SZ, _SZ, _P],
     "cxm_gemm_f32": [_P, _P, _P, _SZ, _SZ, _SZ, _I, _I, _P, _I, _P, _P],
     "cxm_matmul_t": [_P, _P, _P, _SZ, _SZ, _SZ, _I, _P],

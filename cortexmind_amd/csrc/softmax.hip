@@ -25,6 +25,8 @@
 //  * any shape or alignment: wave per row, three sweeps over the row.
 // The running max starts from -FLT_MAX, as reduce::max does, so an
 // all -inf row (or segment) never forms (-inf) - (-inf).
+#include <atomic>
+
 #include "cxm_common.hpp"
 
 namespace cxm {
@@ -349,6 +351,17 @@ constexpr int kXNV = 8;
 constexpr size_t kXSeg = static_cast<size_t>(kBlock) * 4 * kXNV;  // floats per segment
 constexpr size_t kXRowsMax = 8192;
 
+// Staggered start of row groups.  Left alone, every workgroup loads at
+// once, every row then waits for its exchange with HBM idle, and every
+// workgroup stores at once.  Workgroups of row group g (of `groups`) sleep
+// g * quanta times 128 cycles before their first load, so the later groups'
+// loads fill the earlier groups' exchange gap.  Results do not depend on it.
+__device__ __forceinline__ void x_stagger(size_t row, unsigned segs, unsigned groups, unsigned quanta) {
+    const size_t rows = gridDim.x / segs;
+    const unsigned n = static_cast<unsigned>(row * groups / rows) * quanta;
+    for (unsigned i = 0; i < n; ++i) __builtin_amdgcn_s_sleep(2);
+}
+
 __device__ __forceinline__ unsigned long long xld(const unsigned long long *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -422,7 +435,8 @@ __device__ __forceinline__ float dot4(float r, float4 g, float4 y) {
 template <bool LOG>
 __global__ __launch_bounds__(kBlock) void k_sm_fwd_x(const float *__restrict__ x, float *__restrict__ y,
                                                      size_t cols, unsigned segs, unsigned *hdr,
-                                                     unsigned long long *slots, unsigned limit) {
+                                                     unsigned long long *slots, unsigned limit,
+                                                     unsigned groups, unsigned quanta) {
     constexpr int NV = kXNV;
     __shared__ float lds[kWavesPerBlock];
     __shared__ float part[2][kXMaxSegs];
@@ -430,6 +444,7 @@ __global__ __launch_bounds__(kBlock) void k_sm_fwd_x(const float *__restrict__ x
     __shared__ unsigned s_tag;
     const size_t row = blockIdx.x / segs;
     const unsigned seg = blockIdx.x - static_cast<unsigned>(row) * segs;
+    x_stagger(row, segs, groups, quanta);
     const float *__restrict__ xr = x + row * cols;
     const size_t n4 = (cols - static_cast<size_t>(seg) * kXSeg) / 4;
     const float4 ninf = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
@@ -739,6 +754,27 @@ bool use_split(size_t cols) { return cols > kWaveRowMax; }
 // region stays small (rows * 1.25 KiB).
 bool use_x(size_t rows, size_t cols) { return rows <= kXRowsMax && (cols + kXSeg - 1) / kXSeg <= kXMaxSegs; }
 
+// Stagger of the single-pass forward: up to 16 row groups, the last one
+// starting about pct% of the time the input takes to stream in (at 6 TB/s,
+// 2.4 GHz) after the first.  Only when the whole grid is resident at once
+// (at most 1024 workgroups, four per CU); beyond that the dispatch order
+// staggers the rows already.  Measured on gfx950 with 32 MiB inputs
+// (pct 0 -> 60 -> 70): [64, 131072] 14.6 -> 13.9 -> 13.6 us, [128, 65536]
+// 13.3 -> 12.4 -> 12.4, [256, 32768] 13.1 -> 12.1 -> 12.1; at 80 the
+// forward slows again, and an 8 MiB input gains nothing.  The backward
+// (two inputs, one output) was slower at every setting and starts at once.
+std::atomic<int> g_x_stagger_pct{65};
+
+void x_stagger_for(size_t rows, unsigned segs, size_t bytes_in, unsigned *groups, unsigned *quanta) {
+    *groups = 1;
+    *quanta = 0;
+    const int pct = g_x_stagger_pct.load(std::memory_order_relaxed);
+    if (pct <= 0 || rows < 2 || rows * segs > 1024) return;
+    *groups = rows < 16 ? static_cast<unsigned>(rows) : 16u;
+    const double total = static_cast<double>(bytes_in) / 6.0e12 * (pct / 100.0) * 2.4e9 / 128.0;
+    *quanta = static_cast<unsigned>(total / (*groups - 1));
+}
+
 int sm_fwd_x(const float *x, float *y, size_t rows, size_t cols, int log_mode, cxm_stream_t st) {
     const unsigned segs = static_cast<unsigned>((cols + kXSeg - 1) / kXSeg);
     Exchange xc;
@@ -746,10 +782,14 @@ int sm_fwd_x(const float *x, float *y, size_t rows, size_t cols, int log_mode, c
     if (rc) return rc;
     const dim3 grid(static_cast<unsigned>(rows * segs));
     const unsigned lim = exchange_wait_limit();
+    unsigned g, q;
+    x_stagger_for(rows, segs, rows * cols * sizeof(float), &g, &q);
     if (log_mode)
-        hipLaunchKernelGGL(k_sm_fwd_x<true>, grid, dim3(kBlock), 0, hs(st), x, y, cols, segs, xc.hdr, xc.slots, lim);
+        hipLaunchKernelGGL(k_sm_fwd_x<true>, grid, dim3(kBlock), 0, hs(st), x, y, cols, segs, xc.hdr, xc.slots, lim,
+                           g, q);
     else
-        hipLaunchKernelGGL(k_sm_fwd_x<false>, grid, dim3(kBlock), 0, hs(st), x, y, cols, segs, xc.hdr, xc.slots, lim);
+        hipLaunchKernelGGL(k_sm_fwd_x<false>, grid, dim3(kBlock), 0, hs(st), x, y, cols, segs, xc.hdr, xc.slots,
+                           lim, g, q);
     return launch_status();
 }
 
@@ -859,6 +899,13 @@ int softmax_bwd(const float *y, const float *dy, float *dx, size_t rows, size_t 
 using namespace cxm;
 
 extern "C" {
+
+int cxm_softmax_stagger(int pct, int *previous) {
+    if (pct < 0 || pct > 100) return CXM_E_INVALID;
+    const int old = cxm::g_x_stagger_pct.exchange(pct);
+    if (previous) *previous = old;
+    return CXM_OK;
+}
 
 int cxm_softmax_fwd_f32(const float *x, float *y, size_t rows, size_t cols, int log_mode,
                         cxm_stream_t s) {

@@ -299,6 +299,13 @@ int cxm_softmax_bwd_f32(const float *y, const float *dy, float *dx, size_t rows,
  * path).  Process-wide; *previous (if not NULL) gets the old value.  No
  * reference counterpart. */
 int cxm_exchange_wait_limit(unsigned polls, unsigned *previous);
+/* Row-group stagger of the single-pass long-row softmax forward,
+ * process-wide: the last of up to 16 row groups starts about pct% (0..100,
+ * default 65) of the input's streaming time after the first; 0 starts every
+ * workgroup at once.  Results do not depend on it.  The previous value goes
+ * to *previous when not NULL.  For tests and tuning; no reference
+ * counterpart. */
+int cxm_softmax_stagger(int pct, int *previous);
 
 /* ---------------------------------------------------------------- matmul
  * Row-major C[xN, zN] = A[xN, yN] * B[yN, zN]: matrix_t::matmul

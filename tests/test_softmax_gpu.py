@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 from cortexmind_amd import engine
-from cortexmind_amd._lib import call
+from cortexmind_amd._lib import E_INVALID, call, lib
 from cortexmind_amd.data import SplitMix64, c1_softmax, c4_long_softmax
 
 from gpu_util import dev, empty
@@ -181,6 +181,41 @@ def test_single_pass_recompute_is_bit_identical(hip, shape):
             _wait_limit(old)
     for a, b in zip(*outs):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def _stagger(pct):
+    old = ctypes.c_int(0)
+    call("cxm_softmax_stagger", pct, ctypes.byref(old))
+    return old.value
+
+
+@pytest.mark.parametrize("shape", [(64, 16384), (17, 40000), (2, 131072)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_single_pass_stagger_is_bit_identical(hip, shape):
+    """The single-pass forward starts row groups at staggered times; the
+    results (and the backward fed from them) must be the same bits with the
+    stagger off (0), at the default and at its maximum (100)."""
+    r, c = shape
+    g = SplitMix64(11 * r + c)
+    x = g.normal((r, c), 0.0, 8.0)
+    dyv = g.normal((r, c))
+    outs = []
+    for pct in (0, 65, 100):
+        old = _stagger(pct)
+        try:
+            ys = [fwd(x, False), fwd(x, True)]
+            outs.append(ys + [bwd(ys[0], dyv, False), bwd(ys[1], dyv, True)])
+        finally:
+            _stagger(old)
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_stagger_argument(hip):
+    assert lib().cxm_softmax_stagger(101, None) == E_INVALID
+    assert lib().cxm_softmax_stagger(-1, None) == E_INVALID
+    old = _stagger(65)
+    assert _stagger(old) == 65
 
 
 def test_single_pass_epochs_across_shapes(hip, orc):
