@@ -20,6 +20,8 @@
 // MFMA operand layout (32x32x2, one block): lane l supplies A[l%32][l/32]
 // and B[l/32][l%32]; accumulator register r of lane l holds
 // C[8*(r/4) + 4*(l/32) + r%4][l%32].
+#include <atomic>
+
 #include "cxm_common.hpp"
 
 namespace cxm {
@@ -1033,7 +1035,7 @@ __global__ __launch_bounds__(kThinNT) void k_gemm_thin_k(const float *__restrict
 // k-contiguous with BK 32/64, 3/4 four-wave with BK 32/64, 5 k-contiguous
 // without the XCD renumbering, 6 k-major with it, 7 the direct-to-LDS ring
 // (where its shape conditions hold, else 1).
-int g_gemm_kc = -1;
+std::atomic<int> g_gemm_kc{-1};
 
 // Measured on gfx950 (TFLOP/s, best variant vs the others):
 //  * grids of >= 1024 workgroups (8192^3, 4096^3): four waves of 64x64, BK 32
@@ -1047,8 +1049,9 @@ int g_gemm_kc = -1;
 //    4096^3, 135 against 125 at 8192^3; A^T B (split K) measured even and
 //    keeps the k-major kernel.
 inline int gemm_variant(bool ta, bool tb, unsigned wgs, bool ring_ok) {
-    if (g_gemm_kc == 7) return ring_ok ? 7 : 1;
-    if (g_gemm_kc >= 0) return g_gemm_kc;
+    const int pinned = g_gemm_kc.load(std::memory_order_relaxed);
+    if (pinned == 7) return ring_ok ? 7 : 1;
+    if (pinned >= 0) return pinned;
     if (ring_ok && !ta) return 7;
     if (wgs >= 1024) return 3;
     if (ta && !tb) return 6;
@@ -1200,7 +1203,7 @@ int cxm_gemm_f32(const float *a, const float *b, float *c, size_t m, size_t k, s
 
 int cxm_gemm_f32_kernel(int variant) {
     if (variant < -1 || variant > 7) return CXM_E_INVALID;
-    cxm::g_gemm_kc = variant;
+    cxm::g_gemm_kc.store(variant);
     return CXM_OK;
 }
 

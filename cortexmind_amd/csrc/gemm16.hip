@@ -39,6 +39,8 @@
 // The next k step's tiles, loaded into registers at the top of the step,
 // are written to the other LDS buffer three quarters of the way through the
 // step's MFMAs, so one barrier separates two steps.
+#include <atomic>
+
 #include "cxm_common.hpp"
 #include "half.hpp"
 
@@ -881,7 +883,7 @@ int dispatch16(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size
 // g_gemm16_kernel (tests) forces 0 = 128x128 staged, 1 = 256x256 staged,
 // 2 = 256 ring, 3 = 128 ring; a ring whose conditions fail falls back to
 // the staged kernel of its tile size.
-int g_gemm16_kernel = -1;
+std::atomic<int> g_gemm16_kernel{-1};
 constexpr unsigned kRingGroup = 4;
 
 template <int DT, int TM>
@@ -923,8 +925,9 @@ int gemm16(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size_t K
     const bool ring256 = al && M % 256 == 0 && N % 256 == 0;
     const bool ring128 = al && M % 128 == 0 && N % 128 == 0;
     int kernel = big_tiles >= 128 ? (ring256 ? 2 : 1) : (ring128 ? 3 : 0);
-    if (g_gemm16_kernel >= 0) {
-        kernel = g_gemm16_kernel;
+    const int pinned = g_gemm16_kernel.load(std::memory_order_relaxed);
+    if (pinned >= 0) {
+        kernel = pinned;
         if (kernel == 2 && !ring256) kernel = 1;
         if (kernel == 3 && !ring128) kernel = 0;
     }
@@ -964,7 +967,7 @@ int cxm_matmul_t(const void *a, const void *b, void *c, size_t xN, size_t yN, si
 
 int cxm_gemm16_kernel(int kernel) {
     if (kernel < -1 || kernel > 3) return CXM_E_INVALID;
-    cxm::g_gemm16_kernel = kernel;
+    cxm::g_gemm16_kernel.store(kernel);
     return CXM_OK;
 }
 
