@@ -153,7 +153,8 @@ def test_bad_arguments(hip):
     assert lib().cxm_gemm_f32(d.ptr, d.ptr, d.ptr, 4, 4, 4, 0, 0, None, 7, None, None) == E_INVALID
 
 
-@pytest.mark.parametrize("m,k,n,ta,tb", [(4096, 1024, 10, 0, 0), (1024, 4096, 10, 1, 0), (4096, 10, 1024, 0, 1),
+@pytest.mark.parametrize("m,k,n,ta,tb", [(4096, 1024, 10, 0, 0), (300, 512, 16, 0, 0), (129, 1020, 7, 0, 0),
+                                         (65, 4, 12, 0, 0), (1, 1024, 1, 0, 0), (1024, 4096, 10, 1, 0), (4096, 10, 1024, 0, 1),
                                          (4096, 10, 1024, 0, 0), (77, 100, 3, 0, 0), (64, 333, 16, 1, 0),
                                          (50, 16, 36, 0, 1)])
 def test_thin_products(hip, orc, m, k, n, ta, tb):
