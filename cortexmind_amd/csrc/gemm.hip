@@ -60,6 +60,69 @@ __device__ __forceinline__ void store_epi(const Epilogue &e, float *C, size_t ro
     *p = v;
 }
 
+// Writes a lane's WI_ x WJ_ accumulator blocks through the epilogue (same
+// arithmetic as store_epi).  Every memory operand the epilogue reads (the
+// gate, or C's old value for the SGD update, and the bias) is loaded for
+// the whole tile before any result is computed, and the epilogue's options
+// are applied with selects, so a lane whose outputs are all in range runs
+// one straight block: loads, then arithmetic, then stores.  Element by
+// element, each store waited for its own load (a memory round trip per
+// element, 11 us of a 4096 x 1024 x 1024 product with a ReLU gate).
+__device__ __forceinline__ float epi_value(const Epilogue &e, float v, float bias, float pre) {
+    const float t = v * e.lr;  // SGD: matrix_t::sub(W, ScalarOp::mul(G, lr)): two roundings
+    const float sgd = pre - t;
+    float u = e.bias ? v + bias : v;
+    u = (e.act == CXM_ACT_RELU && 0.0f > u) ? 0.0f : u;
+    u = e.gate ? u * (pre > 0.0f ? 1.0f : 0.0f) : u;
+    return e.sgd ? sgd : u;
+}
+
+template <int WI_, int WJ_, class RowF, class ColF>
+__device__ __forceinline__ void store_tile_epi(const floatx16 (&acc)[WI_][WJ_], float *__restrict__ C, size_t M,
+                                               size_t N, RowF row_of, ColF col_of, const Epilogue &e) {
+    const float *pre_src = e.sgd ? C : e.gate;  // both [M, N]
+    bool all_in = true;
+#pragma unroll
+    for (int i = 0; i < WI_; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) all_in = all_in && row_of(i, r) < M;
+#pragma unroll
+    for (int j = 0; j < WJ_; ++j) all_in = all_in && col_of(j) < N;
+    float bias[WJ_];
+#pragma unroll
+    for (int j = 0; j < WJ_; ++j) {
+        const size_t col = col_of(j);
+        bias[j] = (e.bias && !e.sgd && col < N) ? e.bias[col] : 0.0f;
+    }
+    if (all_in) {
+        float pre[WI_][WJ_][16];
+#pragma unroll
+        for (int i = 0; i < WI_; ++i)
+#pragma unroll
+            for (int j = 0; j < WJ_; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    pre[i][j][r] = pre_src ? pre_src[row_of(i, r) * N + col_of(j)] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < WI_; ++i)
+#pragma unroll
+            for (int j = 0; j < WJ_; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    C[row_of(i, r) * N + col_of(j)] = epi_value(e, acc[i][j][r], bias[j], pre[i][j][r]);
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < WI_; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ_; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const size_t row = row_of(i, r), col = col_of(j);
+                if (row < M && col < N) store_epi(e, C, row, col, N, acc[i][j][r]);
+            }
+}
+
 // Loads one 4-element group of the A tile (slot 0..BM*BK/4-1) into registers.
 // Non-transposed A [M,K]: group = 4 consecutive k of one row.
 // Transposed A (stored [K,M]): group = 4 consecutive m of one k.
@@ -159,16 +222,10 @@ __device__ __forceinline__ void gemm_epilogue(floatx16 (&acc)[WI_][WJ_], float *
     auto out_row = [&](int i, int r) { return wm * 32 * WI_ + i * 32 + 8 * (r / 4) + 4 * lhi + (r % 4); };
     auto out_col = [&](int j) { return wn * 32 * WJ_ + j * 32 + l32; };
 
+    auto row_of = [&](int i, int r) { return m0 + out_row(i, r); };
+    auto col_of = [&](int j) { return n0 + out_col(j); };
     if (splits == 1) {
-#pragma unroll
-        for (int i = 0; i < WI_; ++i)
-#pragma unroll
-            for (int j = 0; j < WJ_; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const size_t row = m0 + out_row(i, r), col = n0 + out_col(j);
-                    if (row < M && col < N) store_epi(epi, C, row, col, N, acc[i][j][r]);
-                }
+        store_tile_epi<WI_, WJ_>(acc, C, M, N, row_of, col_of, epi);
         return;
     }
 
@@ -203,15 +260,7 @@ __device__ __forceinline__ void gemm_epilogue(floatx16 (&acc)[WI_][WJ_], float *
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + v[i][j][r];
     }
-#pragma unroll
-    for (int i = 0; i < WI_; ++i)
-#pragma unroll
-        for (int j = 0; j < WJ_; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const size_t row = m0 + out_row(i, r), col = n0 + out_col(j);
-                if (row < M && col < N) store_epi(epi, C, row, col, N, acc[i][j][r]);
-            }
+    store_tile_epi<WI_, WJ_>(acc, C, M, N, row_of, col_of, epi);
 }
 
 template <bool TA, bool TB, bool VA, bool VB, bool XCDMAP = false>
