@@ -1110,15 +1110,16 @@ std::atomic<int> g_gemm_kc{-1};
 //    renumbering (97.5 and 77 against 87-89 and 70-75);
 //  * A B and A B^T at 256-tile grids: k-contiguous tiles, BK 32, with the
 //    renumbering (93 and 104 against 90 and 94 for the k-major kernel).
-//  * the ring (M, N, K multiples of 128, 16-byte aligned bases) for A B and
-//    A B^T: 99-100 against 92-95 at 4096x1024x1024, 133 against 113 at
-//    4096^3, 135 against 125 at 8192^3; A^T B (split K) measured even and
-//    keeps the k-major kernel.
+//  * the ring (M, N, K multiples of 128, 16-byte aligned bases) for A B,
+//    A B^T and A^T B: 99-100 against 92-95 at 4096x1024x1024, 133 against
+//    113 at 4096^3, 135 against 125 at 8192^3; A^T B with K split four ways
+//    (1024x4096x1024) 3-8% faster than the k-major kernel in interleaved
+//    runs.
 inline int gemm_variant(bool ta, bool tb, unsigned wgs, bool ring_ok) {
     const int pinned = g_gemm_kc.load(std::memory_order_relaxed);
     if (pinned == 7) return ring_ok ? 7 : 1;
     if (pinned >= 0) return pinned;
-    if (ring_ok && !ta) return 7;
+    if (ring_ok && !(ta && tb)) return 7;
     if (wgs >= 1024) return 3;
     if (ta && !tb) return 6;
     return 1;
