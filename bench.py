@@ -18,6 +18,9 @@ back-to-back launches of that op alone (rotating inputs).  ``traffic`` is
 the HBM bytes per launch measured with rocprofv3 PMC counters (FETCH_SIZE,
 WRITE_SIZE, scaled against a plain copy kernel), read from
 profiles/pmc_traffic.txt when that file has a line for the kernel.
+``measured_peaks`` (bandwidth headlines) gives the copy and read rates this
+part reaches at 1 GiB, with the value and the roofline figure as fractions
+of the read rate, beside ``frac_of_peak`` against the 8 TB/s specification.
 ``cpu_baseline`` times the C restatement of the reference AVX2 path
 (oracle/, one thread, as the reference is single-threaded) on the same host
 over a bounded sample of whole steps.
@@ -292,6 +295,43 @@ WORKLOADS = {"c1": wl_c1, "c2": wl_c2, "c3": wl_c3, "c4": wl_c4, "c5": wl_c5, "m
 
 # ------------------------------------------------------------------ timing
 
+def measured_peaks(E, D, Event, sync, reps=5):
+    """Measured bandwidth ceilings to read the HBM figures against, beside
+    the 8 TB/s specification, over 1 GiB of fp32: a copy (this library's
+    streaming map z = x * 1, the bytes of a copy; the runtime's
+    device-to-device hipMemcpy is reported beside it and runs slower) and a
+    read (the row sum of [16384, 16384], output 64 KiB), each the mean of
+    `reps` launches between events after two untimed ones."""
+    from cortexmind_amd._lib import OP_MUL, call
+
+    n = 16384
+    a, b, z = D((n * n,)), D((n * n,)), D((n,))
+    call("cxm_memset", a.ptr, 0, a.nbytes, None)
+    res = {}
+    for name, fn, nbytes in [("copy", lambda: call("cxm_scalar_f32", a.ptr, 1.0, b.ptr, n * n, OP_MUL, None),
+                              2 * a.nbytes),
+                             ("hipmemcpy_d2d", lambda: call("cxm_memcpy_d2d", b.ptr, a.ptr, a.nbytes, None),
+                              2 * a.nbytes),
+                             ("read", lambda: E.reduce.sum(a, z, n, n, 1), a.nbytes + z.nbytes)]:
+        for _ in range(2):
+            fn()
+        sync()
+        t0, t1 = Event(), Event()
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        t1.sync()
+        ms = t0.elapsed_ms(t1) / reps
+        t0.close()
+        t1.close()
+        res[f"{name}_GBps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    del a, b, z
+    res["sample"] = ("1 GiB fp32: copy = cxm_scalar_f32 z = x * 1 and hipmemcpy_d2d = cxm_memcpy_d2d (bytes read + "
+                     f"written), read = row sum of [16384, 16384]; mean of {reps} launches each")
+    return res
+
+
 def time_steps(ops, steps, warmup, Event, sync):
     """Whole steps: warm-up, then events around `steps` steps."""
     k = 0
@@ -499,6 +539,10 @@ def main():
     }
     if head["unit"] == "GB/s":
         out["frac_of_peak"] = round(head["value"] / PEAK_HBM_GBS, 4)
+        mp = measured_peaks(E, D, Event, sync)
+        mp["value_frac_of_read"] = round(head["value"] / mp["read_GBps"], 4)
+        mp["roofline_frac_of_read"] = round(head["roofline"]["achieved"] / mp["read_GBps"], 4)
+        out["measured_peaks"] = mp
     if not args.no_cpu and args.workload == "c2":
         out["cpu_baseline"] = cpu_c2(head["host"], args.cpu_seconds)
     if args.workload == "g16" and torch_ok:
