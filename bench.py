@@ -554,6 +554,8 @@ def main():
             wl[name] = {"workload": r["config"]["workload"], "value": round(r["value"], 2),
                         "unit": r["unit"], "ms_per_step": round(r["ms_per_step"], 5),
                         "roofline": r["roofline"], "per_op": r["per_op"]}
+            if r["unit"] == "GB/s" and "measured_peaks" in out:
+                wl[name]["frac_of_measured_copy"] = round(r["value"] / out["measured_peaks"]["copy_GBps"], 4)
         out["workloads"] = wl
     print(json.dumps(out), flush=True)
 
