@@ -98,10 +98,10 @@ def wl_c2(E, D):
         Op("mean_axis1", "k_rows<SumOp,true,4>", rot(lambda b: R.mean(b, zf, rows, cols, 1)), xb + 4 * rows),
         Op("max_axis1", "k_rows<MaxOp,true,4>", rot(lambda b: R.max(b, zf, rows, cols, 1)), xb + 4 * rows),
         Op("argmax_axis1", "k_rows<ArgMaxOp,true,4>", rot(lambda b: R.argmax(b, zi, rows, cols, 1)), xb + 4 * rows),
-        Op("sum_axis0", "k_cols<SumOp,true,8,16>", rot(lambda b: R.sum(b, zf, 1, rows, cols)), xb + 4 * cols),
-        Op("mean_axis0", "k_cols<SumOp,true,8,16>", rot(lambda b: R.mean(b, zf, 1, rows, cols)), xb + 4 * cols),
-        Op("max_axis0", "k_cols<MaxColOp,true,8,16>", rot(lambda b: R.max(b, zf, 1, rows, cols)), xb + 4 * cols),
-        Op("argmax_axis0", "k_cols<ArgMaxOp,true,8,16>", rot(lambda b: R.argmax(b, zi, 1, rows, cols)), xb + 4 * cols),
+        Op("sum_axis0", "k_cols<SumOp,true,16,16>", rot(lambda b: R.sum(b, zf, 1, rows, cols)), xb + 4 * cols),
+        Op("mean_axis0", "k_cols<SumOp,true,16,16>", rot(lambda b: R.mean(b, zf, 1, rows, cols)), xb + 4 * cols),
+        Op("max_axis0", "k_cols<MaxColOp,true,16,16>", rot(lambda b: R.max(b, zf, 1, rows, cols)), xb + 4 * cols),
+        Op("argmax_axis0", "k_cols<ArgMaxOp,true,16,16>", rot(lambda b: R.argmax(b, zi, 1, rows, cols)), xb + 4 * cols),
     ]
     desc = {"workload": "C2 reductions fp32 [4096,4096] ~ U(-1,1)", "shape": [rows, cols],
             "ops": [o.name for o in ops], "rotating_input_buffers": nbuf, "buffer_bytes": xb}

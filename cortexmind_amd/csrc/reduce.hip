@@ -352,7 +352,12 @@ int run_cols_plan(const float *x, size_t outer, size_t dim, size_t inner, OutDes
     hipLaunchKernelGGL((k_cols<Op, VEC_, UNR_, NW_>), dim3(nb), dim3(NW_ * kWave), 0, hs, x, dim, inner, \
                        nt, nc, rpc, plan.tile_major, part, counters, out)
     if (plan.nw == 16) {
-        if (vec) CXM_COLS(true, UNRC, 16);
+        // With a multiple of 16 rows per wave, all 16 loads of a batch are in
+        // flight together (C2's column reductions: 13.4 against 13.8 us with
+        // batches of 8); other chunk sizes keep batches of UNRC, since rows
+        // past the last whole batch load one at a time.
+        if (vec && (rpc / 16) % 16 == 0) CXM_COLS(true, 16, 16);
+        else if (vec) CXM_COLS(true, UNRC, 16);
         else CXM_COLS(false, 1, 16);
     } else {
         if (vec) CXM_COLS(true, UNRC, 4);
