@@ -857,9 +857,26 @@ int sm_bwd_split(const float *y, const float *dy, float *dx, size_t rows, size_t
     return launch_status();
 }
 
+// [a, a + bytes) and [b, b + bytes) share at least one byte.
+bool overlaps(const void *a, const void *b, size_t bytes) {
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    return pa < pb + bytes && pb < pa + bytes;
+}
+
+// Aliasing rules of the softmax entry points.  An output may be one of the
+// inputs exactly (in place): every kernel but the single-pass long-row one
+// reads an element in the thread that later writes it, and the single-pass
+// kernel, whose waiting workgroups may re-read a peer's input segment, is
+// not used in place (the two-pass kernels run instead).  Any other overlap
+// is rejected.
+bool bad_alias(const void *out, const void *in, size_t bytes) { return out != in && overlaps(out, in, bytes); }
+
 int softmax_fwd(const float *x, float *y, size_t rows, size_t cols, int log_mode, cxm_stream_t st) {
     if (!x || !y || (log_mode != 0 && log_mode != 1)) return CXM_E_INVALID;
     if (rows == 0 || cols == 0) return CXM_OK;
+    if (rows > SIZE_MAX / sizeof(float) / cols) return CXM_E_TOO_LARGE;
+    const size_t bytes = rows * cols * sizeof(float);
+    if (bad_alias(y, x, bytes)) return CXM_E_INVALID;
     hipStream_t s = hs(st);
     const bool vec = cols % 4 == 0 && aligned16(x) && aligned16(y);
     if (!vec) {
@@ -870,7 +887,7 @@ int softmax_fwd(const float *x, float *y, size_t rows, size_t cols, int log_mode
     }
     if (!use_split(cols))
         return log_mode ? sm_fwd_wave<true>(x, y, rows, cols, s) : sm_fwd_wave<false>(x, y, rows, cols, s);
-    if (use_x(rows, cols)) return sm_fwd_x(x, y, rows, cols, log_mode, st);
+    if (use_x(rows, cols) && x != y) return sm_fwd_x(x, y, rows, cols, log_mode, st);
     return sm_fwd_split<kSegNV>(x, y, rows, cols, log_mode, st);
 }
 
@@ -878,6 +895,9 @@ int softmax_bwd(const float *y, const float *dy, float *dx, size_t rows, size_t 
                 cxm_stream_t st) {
     if (!y || !dy || !dx || (log_mode != 0 && log_mode != 1)) return CXM_E_INVALID;
     if (rows == 0 || cols == 0) return CXM_OK;
+    if (rows > SIZE_MAX / sizeof(float) / cols) return CXM_E_TOO_LARGE;
+    const size_t bytes = rows * cols * sizeof(float);
+    if (bad_alias(dx, y, bytes) || bad_alias(dx, dy, bytes)) return CXM_E_INVALID;
     hipStream_t s = hs(st);
     const bool vec = cols % 4 == 0 && aligned16(y) && aligned16(dy) && aligned16(dx);
     if (!vec) {
@@ -889,7 +909,7 @@ int softmax_bwd(const float *y, const float *dy, float *dx, size_t rows, size_t 
     if (!use_split(cols))
         return log_mode ? sm_bwd_wave<true>(y, dy, dx, rows, cols, s)
                         : sm_bwd_wave<false>(y, dy, dx, rows, cols, s);
-    if (use_x(rows, cols)) return sm_bwd_x(y, dy, dx, rows, cols, log_mode, st);
+    if (use_x(rows, cols) && dx != y && dx != dy) return sm_bwd_x(y, dy, dx, rows, cols, log_mode, st);
     return sm_bwd_split<kSegNV>(y, dy, dx, rows, cols, log_mode, st);
 }
 

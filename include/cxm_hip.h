@@ -284,7 +284,10 @@ int cxm_affine_act_bwd_f32(const float *x, const float *scale, const float *y, c
  * of [rows, cols].  The reference has none; it is the composition
  * m = reduce::max (reduce.cpp:204-215), z = Broadcast::col::sub(x, m),
  * e = exp(z), s = reduce::sum(e), y = Broadcast::col::div(e, s) or z - log(s).
- * -inf entries give exactly 0 (softmax) and -inf (log-softmax). */
+ * -inf entries give exactly 0 (softmax) and -inf (log-softmax).
+ * y may be x itself (in place); an output that overlaps an input in any
+ * other way is CXM_E_INVALID.  The same holds for dx against y and dy in
+ * the backward. */
 int cxm_softmax_fwd_f32(const float *x, float *y, size_t rows, size_t cols, int log_mode,
                         cxm_stream_t s);
 /* Backward from the saved output y: softmax dx = y*(dy - sum(dy*y));

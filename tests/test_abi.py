@@ -72,6 +72,20 @@ def test_bad_enums_rejected_on_host():
     assert lib.cxm_gemm_f32(p, p, p, 4, 4, 4, 0, 0, None, _lib.ACT_SIGMOID, None, None) == _lib.E_INVALID
 
 
+def test_softmax_partial_overlap_rejected_on_host():
+    """A softmax output that overlaps an input without being it is refused
+    before any launch; exact in-place calls are accepted (run on the GPU in
+    tests/test_softmax_gpu.py)."""
+    lib = _lib.lib()
+    x = ctypes.c_void_p(0x10000)
+    y = ctypes.c_void_p(0x10000 + 16)  # one float4 into x's 4x64 floats
+    assert lib.cxm_softmax_fwd_f32(x, y, 4, 64, 0, None) == _lib.E_INVALID
+    assert lib.cxm_softmax_fwd_f32(y, x, 4, 64, 1, None) == _lib.E_INVALID
+    far = ctypes.c_void_p(0x10000 + 4 * 4 * 64 * 2)
+    assert lib.cxm_softmax_bwd_f32(x, far, y, 4, 64, 0, None) == _lib.E_INVALID
+    assert lib.cxm_softmax_bwd_f32(far, x, y, 4, 64, 1, None) == _lib.E_INVALID
+
+
 def test_empty_outputs_are_noops():
     lib = _lib.lib()
     p = ctypes.c_void_p(0x1000)

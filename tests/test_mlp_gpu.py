@@ -61,11 +61,31 @@ def test_mlp_float64_fixture(hip):
         assert np.max(np.abs(final[k] - FIX[f"mlp_final_{k}"])) <= 1e-5 * (np.abs(FIX[f"mlp_final_{k}"]).max() + 1e-3), k
 
 
-def test_mlp_full_size_ten_steps(hip):
-    """C5 at full size: batch 4096, 10 SGD steps; loss finite and falling,
-    first loss close to ln(10) for He-normal weights on U(0,1) inputs."""
+def test_mlp_full_size_ten_steps_vs_oracle(hip, orc):
+    """C5 exactly as configured: batch 4096, 784 -> 1024 -> 1024 -> 10, He-normal
+    weights, zero biases, 10 SGD steps at lr 0.01, against the oracle's step
+    (about 3 s per step on one CPU core).  At this batch the weight gradients
+    take the split-K kernels with the fused SGD epilogue, which the reduced
+    batch does not reach.  Every step's loss within 1e-5 relative; all six
+    tensors after step 10 within 1e-4 of their scale."""
     x, labels, params = c5_mlp()
     losses, final = gpu_steps(x, labels, params, 0.01, 10)
-    assert all(np.isfinite(losses))
-    assert losses[-1] < losses[0]
-    assert all(np.all(np.isfinite(v)) for v in final.values())
+    ref = {k: v.copy() for k, v in params.items()}
+    ref_losses = []
+    for step in range(10):
+        ref_losses.append(orc.mlp_step(x, labels, ref, 0.01))
+        print(f"step {step}: gpu {losses[step]:.8f} oracle {ref_losses[step]:.8f}", flush=True)
+    for got, want in zip(losses, ref_losses):
+        assert abs(got - want) <= 1e-5 * abs(want), (losses, ref_losses)
+    # A layer's bias moves under the same gradient magnitudes as its weight
+    # (b_l's gradient is a column sum of the same dZ_l that forms W_l's), so
+    # both are held to 1e-4 of that layer's weight scale; the bias itself
+    # starts at zero and stays near 1e-3, where its column sums cancel.
+    errs = {}
+    for k in ref:
+        w = "w" + k[1]
+        scale = max(np.abs(params[w]).max(), np.abs(ref[w]).max())
+        errs[k] = (float(np.max(np.abs(final[k] - ref[k]))), 1e-4 * float(scale))
+        print(f"{k}: max |gpu - oracle| {errs[k][0]:.3e} (bar {errs[k][1]:.3e})", flush=True)
+    assert all(e <= bar for e, bar in errs.values()), errs
+    assert all(np.isfinite(losses)) and losses[-1] < losses[0]

@@ -85,6 +85,38 @@ def test_c2_axis(hip, orc, c2, op, axis):
     check(op, c2, sizes, orc)
 
 
+@pytest.mark.parametrize("n", [4096 * 4096, 4096 * 4096 + 3, 1 << 22])
+def test_global_sum_exact_integers(hip, n):
+    """Full-size global sum and mean of integers in {-1, 0, 1}: every partial
+    sum is an integer below 2^24 in magnitude, so each is exact in fp32 and
+    the result must equal the exact sum bit for bit.  A lost or doubled
+    segment partial (std ~52 for 8192 such terms) cannot hide under this bar,
+    where it could under the 1e-5 * sum|x| tolerance of U(-1, 1) data.
+    Flat and (1, n, 1) forms; the odd length also runs the scalar tail."""
+    r = SplitMix64(0xE1 + n).next_u64(n)
+    x = ((r % np.uint64(3)).astype(np.int64) - 1).astype(np.float32)
+    exact = int(np.sum(x.astype(np.int64)))
+    assert abs(exact) < (1 << 24)
+    for sizes in [(n,), (1, n, 1)]:
+        got = gpu_reduce("sum", x, sizes)
+        assert got[0] == np.float32(exact), (sizes, float(got[0]), exact)
+        mean = gpu_reduce("mean", x, sizes)
+        # flat: sum / (float)N; axis with one output: the division tail
+        want = np.float32(exact) / np.float32(n)
+        assert mean[0] == want, (sizes, float(mean[0]), float(want))
+
+
+@pytest.mark.parametrize("sizes", [(4096, 4096, 1), (1, 4096, 4096), (3, 1000, 257)])
+def test_axis_sum_exact_integers(hip, sizes):
+    """Row and column sums of integers in {-1, 0, 1}: exact, bit for bit."""
+    o, d, i = sizes
+    r = SplitMix64(0xE2 + d).next_u64(o * d * i)
+    x = ((r % np.uint64(3)).astype(np.int64) - 1).astype(np.float32).reshape(o, d, i)
+    exact = x.astype(np.int64).sum(axis=1).ravel().astype(np.float32)
+    got = gpu_reduce("sum", x, sizes)
+    assert np.array_equal(got, exact), sizes
+
+
 def test_c2_deterministic(hip, c2):
     a = gpu_reduce("sum", c2, (c2.size,))
     b = gpu_reduce("sum", c2, (c2.size,))

@@ -293,3 +293,37 @@ def test_xent_bad_label_gives_nan(hip):
     a, b_, c_, d_ = dev(logits), dev(labels), empty((1,)), empty((300, 4))
     engine.train.softmax_xent(a, b_, c_, d_, 300, 4)
     assert np.isnan(c_.numpy()[0])
+
+
+@pytest.mark.parametrize("shape,same_path", [((64, 1024), True), ((16, 40000), False), ((8, 600000), True),
+                                              ((5, 37), True)])
+@pytest.mark.parametrize("log", [False, True])
+def test_in_place(hip, orc, shape, same_path, log):
+    """y == x (forward) and dx == dy / dx == y (backward) against the oracle,
+    on every path: the wave kernel, the single-pass long-row shape (which in
+    place runs the two-pass kernels instead), the two-pass shape and the
+    unaligned kernel.  Where the path is the same as out of place, the bits
+    are too."""
+    g = SplitMix64(0x1A1A + shape[1])
+    x = g.normal(shape, 0.0, 4.0)
+    dy_h = g.normal(shape, 0.0, 1.0)
+    r, c = shape
+    sep = fwd(x, log)
+    buf = dev(x)
+    engine.softmax.forward(buf, buf, r, c, log=log)
+    got = buf.numpy()
+    # past F64_COLS columns the oracle's own fp32 row sums drift beyond the
+    # bar, so the float64 closed form is the reference there (as in test_shapes)
+    check_fwd(x, got, orc.softmax_fwd(x, log) if c <= F64_COLS else f64_fwd(x, log), log)
+    if same_path:
+        assert np.array_equal(got.view(np.uint32), sep.view(np.uint32))
+    want = bwd(sep, dy_h, log)
+    ref = orc.softmax_bwd(sep, dy_h, log) if c <= F64_COLS else f64_bwd(sep, dy_h, log)
+    for alias in ("dy", "y"):
+        dy_d, dg = dev(sep), dev(dy_h)
+        out = dg if alias == "dy" else dy_d
+        engine.softmax.backward(dy_d, dg, out, r, c, log=log)
+        got = out.numpy()
+        check_bwd(sep, dy_h, got, ref, log)
+        if same_path:
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), alias
