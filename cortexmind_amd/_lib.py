@@ -75,6 +75,7 @@ SIGNATURES = {
     "cxm_reduce_max_flat_f32": [_P, _P, _SZ, _P],
     "cxm_reduce_argmax_flat_f32": [_P, _P, _SZ, _P],
     "cxm_reduce_sum_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
+    "cxm_reduce_sum_noalloc_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
     "cxm_reduce_mean_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
     "cxm_reduce_max_f32": [_P, _P, _SZ, _SZ, _SZ, _P],
     "cxm_reduce_argmax_f32": [_P, _P, _SZ, _SZ, _SZ, _P],

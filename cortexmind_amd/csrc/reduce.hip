@@ -17,12 +17,78 @@
 //    slice and a chunk of the reduced rows; each thread keeps one float4 of
 //    columns, the four waves take interleaved rows and meet in LDS.  Chunks
 //    are combined in chunk order by the last workgroup of the column tile.
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "cxm_common.hpp"
 
+// Scratch of cxm_reduce_sum_noalloc_f32: ticket counters first (kCtr words
+// each), then partial results.  One copy per device, held until the process
+// ends.  Host code never passes this name to a kernel: the address of each
+// device's copy comes from hipGetSymbolAddress (fixed_scratch below).
+constexpr size_t kFixedCounterBytes = size_t(1) << 20;  // 4096 counters
+constexpr size_t kFixedPartBytes = size_t(1) << 20;
+static __device__ __align__(256) unsigned char scratch[kFixedCounterBytes + kFixedPartBytes];
+
 namespace cxm {
 namespace {
+
+__global__ void k_zero_words(unsigned *p, size_t n) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x)
+        p[i] = 0u;
+}
+
+constexpr int kMaxDevices = 64;
+std::atomic<unsigned char *> g_fixed[kMaxDevices];
+std::mutex g_fixed_mu;
+
+// Device address of the current device's `scratch`, looked up once per
+// device (with that device current) on its first use; the counters are
+// then cleared by a fill kernel on stream s.  Every kernel that takes a
+// ticket puts its counter back to zero, so they stay clear between calls.
+int fixed_scratch(cxm_stream_t s, unsigned char **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (dev < 0 || dev >= kMaxDevices) return CXM_E_TOO_LARGE;
+    unsigned char *p = g_fixed[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lk(g_fixed_mu);
+        p = g_fixed[dev].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            void *a = nullptr;
+            e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return static_cast<int>(e);
+            if (a == nullptr) return CXM_E_INVALID;
+            hipLaunchKernelGGL(k_zero_words, dim3(256), dim3(256), 0, reinterpret_cast<hipStream_t>(s),
+                               static_cast<unsigned *>(a), kFixedCounterBytes / sizeof(unsigned));
+            e = hipGetLastError();
+            if (e != hipSuccess) return static_cast<int>(e);
+            p = static_cast<unsigned char *>(a);
+            g_fixed[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return CXM_OK;
+}
+
+// Scratch for one launch: the per-stream workspace (allocated on demand),
+// or with `fixed` the static region, for callers that cannot allocate.
+int acquire(bool fixed, cxm_stream_t s, size_t counters, size_t bytes, Workspace *ws) {
+    if (!fixed) return get_workspace(s, counters, bytes, ws);
+    if (counters * kCtr * sizeof(unsigned) > kFixedCounterBytes || bytes > kFixedPartBytes)
+        return CXM_E_TOO_LARGE;
+    unsigned char *base = nullptr;
+    const int rc = fixed_scratch(s, &base);
+    if (rc) return rc;
+    ws->counters = reinterpret_cast<unsigned *>(base);
+    ws->counters_n = kFixedCounterBytes / (kCtr * sizeof(unsigned));
+    ws->scratch = base + kFixedCounterBytes;
+    ws->scratch_bytes = kFixedPartBytes;
+    return CXM_OK;
+}
 
 // Max / min over a column path start from the first slice (reduce.cpp:
 // 230-236, 285-293), which is the same as starting from -inf / +inf.
@@ -257,7 +323,7 @@ __global__ void k_fill_f32(float *z, float v) { *z = v; }
 constexpr unsigned kTargetBlocks = 2048;
 
 template <class Op, int UNRV = 8>
-int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t s, size_t seg_floats = 0) {
+int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t s, bool fixed = false) {
     using T = typename Op::T;
     hipStream_t hs = reinterpret_cast<hipStream_t>(s);
     const bool vec = aligned16(x) && dim % 4 == 0;
@@ -271,7 +337,6 @@ int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t 
         if (segs == 0) segs = 1;
     }
     size_t seg_len = (dim + segs - 1) / segs;
-    if (seg_floats) seg_len = seg_floats;
     seg_len = (seg_len + 1023) / 1024 * 1024;
     segs = seg_len ? (dim + seg_len - 1) / seg_len : 1;
     if (segs == 0) segs = 1;
@@ -283,7 +348,7 @@ int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t 
     if (segs > 1) {
         Workspace ws;
         const size_t nctr = segs <= kTicketGroups ? rows : rows * (kTicketGroups + 1);
-        int rc = get_workspace(s, nctr, rows * segs * sizeof(T), &ws);
+        int rc = acquire(fixed, s, nctr, rows * segs * sizeof(T), &ws);
         if (rc) return rc;
         part = static_cast<T *>(ws.scratch);
         counters = ws.counters;
@@ -323,7 +388,7 @@ ColPlan col_plan(size_t tiles, size_t dim) {
 
 template <class Op, int UNRC = 8>
 int run_cols_plan(const float *x, size_t outer, size_t dim, size_t inner, OutDesc out, ColPlan plan,
-                  cxm_stream_t s) {
+                  cxm_stream_t s, bool fixed = false) {
     using T = typename Op::T;
     hipStream_t hs = reinterpret_cast<hipStream_t>(s);
     const bool vec = aligned16(x) && inner % 4 == 0;
@@ -341,7 +406,7 @@ int run_cols_plan(const float *x, size_t outer, size_t dim, size_t inner, OutDes
     unsigned *counters = nullptr;
     if (chunks > 1) {
         Workspace ws;
-        int rc = get_workspace(s, tiles, tiles * chunks * kColTile * sizeof(T), &ws);
+        int rc = acquire(fixed, s, tiles, tiles * chunks * kColTile * sizeof(T), &ws);
         if (rc) return rc;
         part = static_cast<T *>(ws.scratch);
         counters = ws.counters;
@@ -368,9 +433,10 @@ int run_cols_plan(const float *x, size_t outer, size_t dim, size_t inner, OutDes
 }
 
 template <class Op>
-int run_cols(const float *x, size_t outer, size_t dim, size_t inner, OutDesc out, cxm_stream_t s) {
+int run_cols(const float *x, size_t outer, size_t dim, size_t inner, OutDesc out, cxm_stream_t s,
+             bool fixed = false) {
     const size_t tiles = (inner + kColTile - 1) / kColTile * outer;
-    return run_cols_plan<Op>(x, outer, dim, inner, out, col_plan(tiles, dim), s);
+    return run_cols_plan<Op>(x, outer, dim, inner, out, col_plan(tiles, dim), s, fixed);
 }
 
 enum Which { kSum, kMean, kMax, kArgMax, kMin, kArgMin, kNorm1, kNorm2, kVar, kStdv };
@@ -421,6 +487,17 @@ int reduce_axis(Which which, const float *x, void *z, size_t outer, size_t dim, 
         case kNorm2: return run_cols<SqSumOp>(x, outer, dim, inner, out, s);
         default: return run_cols<Pow2Op>(x, outer, dim, inner, out, s);
     }
+}
+
+// cxm_reduce_sum_f32 with its scratch in the static region: the same
+// checks, plan and kernels, so the same bits.
+int reduce_sum_fixed(const float *x, float *z, size_t outer, size_t dim, size_t inner, cxm_stream_t s) {
+    if (!x || !z) return CXM_E_INVALID;
+    if (outer == 0 || inner == 0) return CXM_OK;
+    if (dim == 0) return CXM_E_INVALID;
+    OutDesc out{z, kOutValue, 0, 1.0f / static_cast<float>(dim), static_cast<float>(dim)};
+    if (inner == 1) return run_rows<SumOp>(x, outer, dim, out, s, true);
+    return run_cols<SumOp>(x, outer, dim, inner, out, s, true);
 }
 
 int reduce_flat(Which which, const float *x, void *z, size_t n, cxm_stream_t s) {
@@ -494,6 +571,11 @@ int cxm_reduce_max_f32(const float *x, float *z, size_t outer, size_t dim, size_
 int cxm_reduce_argmax_f32(const float *x, int32_t *z, size_t outer, size_t dim, size_t inner,
                           cxm_stream_t s) {
     return cxm::reduce_axis(cxm::kArgMax, x, z, outer, dim, inner, s);
+}
+
+int cxm_reduce_sum_noalloc_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                               cxm_stream_t s) {
+    return cxm::reduce_sum_fixed(x, z, outer, dim, inner, s);
 }
 
 #define CXM_REDUCE_ENTRY(NAME, WHICH, ZT)                                                            \

@@ -158,6 +158,20 @@ int cxm_reduce_max_f32(const float *x, float *z, size_t outer, size_t dim, size_
                        cxm_stream_t s);
 int cxm_reduce_argmax_f32(const float *x, int32_t *z, size_t outer, size_t dim, size_t inner,
                           cxm_stream_t s);
+/* cxm_reduce_sum_f32 for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Same arguments, kernels and bits as
+ * cxm_reduce_sum_f32 (the flat sum is (1, n, 1)); its partial sums and
+ * ticket counters live in a static 2 MiB region per device (1 MiB of
+ * counters, 1 MiB of partials) instead of the per-stream workspace, and it
+ * calls no hipMalloc or hipFree.  That region covers every shape the
+ * reduction plan produces; a shape needing more gives CXM_E_TOO_LARGE.  The
+ * first call on a device looks the region up and clears its counters with a
+ * kernel on stream s.  All calls on one device share the region: two calls
+ * that overlap in time on one device (different streams, or host threads)
+ * race and must be serialised by the caller. */
+int cxm_reduce_sum_noalloc_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
+                               cxm_stream_t s);
 /* The rest of avx2::reduce (Engine/AVX2/reduce.hpp:96-329), same two forms:
  *  - min (reduce.cpp:253-309): smallest value; the flat and row forms start
  *    from FLT_MAX (an all-+inf input gives FLT_MAX), the column form from
