@@ -115,6 +115,7 @@ SIGNATURES = {
     "cxm_gemm_f32_kernel": [_I],
     "cxm_softmax_xent_f32": [_P, _P, _P, _P, _SZ, _SZ, _P],
     "cxm_sgd_f32": [_P, _P, _F, _SZ, _P],
+    "cxm_reduce_sum_bwd_f32": [_P, _P, _SZ, _SZ, _SZ, _I, _P],
     "cxm_mlp3_create": [ctypes.POINTER(_P), _SZ, _SZ, _SZ, _SZ, _SZ],
     "cxm_mlp3_step_f32": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P],
     "cxm_mlp3_destroy": [_P],

@@ -477,6 +477,50 @@ int affine_bwd_t(const float *x, const float *scale, const float *y, const float
     return affine_bwd_plan<ACT>(x, scale, y, dy, dx, dscale, dbias, m, n, AffBwdPlan{0, 1}, st);
 }
 
+// ------------------------------------------------- sum / mean backward
+
+// dx[o, d, i] = g(dz[o, i]) over dx as row-major [outer, dim, inner], with
+// g(v) = v for a sum and v / dim for a mean.  One float4 of dx per thread
+// (the grid of k_map4).  MODE 0: inner == 1 and dim % 4 == 0, so a float4
+// lies in one row o and repeats dz[o]; MODE 1: inner % 4 == 0, a float4 is
+// four consecutive inner indices of one (o, d), read as a float4 of dz;
+// MODE 2: any shape or alignment, element by element.
+template <bool MEAN, int MODE>
+__global__ __launch_bounds__(kBlock) void k_sum_bwd(const float *__restrict__ dz, float *__restrict__ dx, size_t dim,
+                                                    size_t inner, size_t n, float dimf) {
+    const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const size_t e = 4 * t;
+    if (e >= n) return;
+    auto g = [dimf](float v) { return MEAN ? v / dimf : v; };
+    if constexpr (MODE == 0) {
+        const float v = g(dz[e / dim]);
+        st4_stream(dx + e, make_float4(v, v, v, v));
+    } else if constexpr (MODE == 1) {
+        const size_t slab = dim * inner;
+        const size_t o = e / slab, i = e % inner;
+        const float4 v = ld4(dz + o * inner + i);
+        st4_stream(dx + e, make_float4(g(v.x), g(v.y), g(v.z), g(v.w)));
+    } else {
+        const size_t slab = dim * inner;
+        for (size_t k = e; k < e + 4 && k < n; ++k) dx[k] = g(dz[(k / slab) * inner + k % inner]);
+    }
+}
+
+template <bool MEAN>
+int sum_bwd_t(const float *dz, float *dx, size_t outer, size_t dim, size_t inner, hipStream_t s) {
+    const size_t n = outer * dim * inner;
+    const unsigned grid = map4_grid(n + 3);
+    if (!grid) return CXM_E_TOO_LARGE;
+    const float dimf = static_cast<float>(dim);
+    if (aligned16(dx) && inner == 1 && dim % 4 == 0)
+        hipLaunchKernelGGL((k_sum_bwd<MEAN, 0>), dim3(grid), dim3(kBlock), 0, s, dz, dx, dim, inner, n, dimf);
+    else if (aligned16(dx) && aligned16(dz) && inner % 4 == 0)
+        hipLaunchKernelGGL((k_sum_bwd<MEAN, 1>), dim3(grid), dim3(kBlock), 0, s, dz, dx, dim, inner, n, dimf);
+    else
+        hipLaunchKernelGGL((k_sum_bwd<MEAN, 2>), dim3(grid), dim3(kBlock), 0, s, dz, dx, dim, inner, n, dimf);
+    return launch_status();
+}
+
 }  // namespace
 }  // namespace cxm
 
@@ -580,6 +624,14 @@ int cxm_act_bwd_f32(const float *y, const float *dy, float *dx, size_t n, int ac
                                y, dy, dx, n);
     }
     return launch_status();
+}
+
+int cxm_reduce_sum_bwd_f32(const float *dz, float *dx, size_t outer, size_t dim, size_t inner, int mean,
+                           cxm_stream_t s) {
+    if (!dz || !dx || (mean != 0 && mean != 1)) return CXM_E_INVALID;
+    if (outer == 0 || dim == 0 || inner == 0) return CXM_OK;
+    if (outer > SIZE_MAX / dim / inner) return CXM_E_TOO_LARGE;
+    return mean ? sum_bwd_t<true>(dz, dx, outer, dim, inner, hs(s)) : sum_bwd_t<false>(dz, dx, outer, dim, inner, hs(s));
 }
 
 int cxm_sgd_f32(float *w, const float *g, float lr, size_t n, cxm_stream_t s) {

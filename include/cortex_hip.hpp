@@ -18,6 +18,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -36,6 +37,136 @@ inline void check(int status, const char *what) {
     if (status != CXM_OK) {
         std::fprintf(stderr, "[ERROR] %s: %s\n", what, cxm_error_string(status));
         std::exit(1);
+    }
+}
+
+// The reference's DeviceType (Memory/type.hpp:22-26) with the HIP device
+// this backend adds.
+enum class DeviceType : std::uint8_t { Unknown = 0, HOST = 1, CUDA = 2, HIP = 3 };
+
+// Type/dtype.hpp:21-33 (same values).
+enum class DType : std::uint8_t {
+    Unknown = 0,
+    Int32 = 1,
+    Int64 = 2,
+    Float32 = 3,
+    Float64 = 4,
+    BFloat16 = 5,
+    Float16 = 6,
+    QInt16 = 7,
+    QInt8 = 8,
+    QUInt16 = 9,
+    QUInt8 = 10,
+};
+
+// Tools/view.hpp:25-83: non-owning view of `size` elements of `type`.
+class TensorView {
+public:
+    TensorView(std::byte *data, DType type, DeviceType device, std::size_t size)
+        : m_data(data), m_type(type), m_device(device), m_size(size) {}
+    TensorView(TensorView const &) = delete;
+    TensorView(TensorView &&) = delete;
+    TensorView &operator=(TensorView const &) = delete;
+    TensorView &operator=(TensorView &&) = delete;
+    ~TensorView() = default;
+
+    [[nodiscard]] std::byte *data() noexcept { return m_data; }
+    [[nodiscard]] const std::byte *data() const noexcept { return m_data; }
+    [[nodiscard]] DType dtype() const noexcept { return m_type; }
+    [[nodiscard]] DeviceType device() const noexcept { return m_device; }
+    [[nodiscard]] std::size_t size() const noexcept { return m_size; }
+
+private:
+    std::byte *m_data;
+    DType m_type;
+    DeviceType m_device;
+    std::size_t m_size;
+};
+
+namespace nv_detail {
+
+[[noreturn]] inline void fail(const char *what, const char *why) {
+    std::fprintf(stderr, "[ERROR] %s: %s\n", what, why);
+    std::exit(1);
+}
+
+// view.hpp:107-117's dispatch, as the ABI's dtype code.
+inline int code(const TensorView &v, const char *what) {
+    if (v.device() != DeviceType::HIP) fail(what, "view is not HIP device memory");
+    switch (v.dtype()) {
+        case DType::Float32: return CXM_DT_F32;
+        case DType::BFloat16: return CXM_DT_BF16;
+        case DType::Float16: return CXM_DT_F16;
+        default: fail(what, "unsupported DType");
+    }
+}
+
+inline int same(const TensorView &a, const TensorView &b, const char *what) {
+    const int c = code(a, what);
+    if (code(b, what) != c) fail(what, "operands differ in dtype");
+    if (a.size() != b.size()) fail(what, "operands differ in element count");
+    return c;
+}
+
+inline int same(const TensorView &a, const TensorView &b, const TensorView &c, const char *what) {
+    same(a, b, what);
+    return same(a, c, what);
+}
+
+inline void unary(const TensorView &Xx, TensorView &Xz, int fn, const char *what) {
+    const int dt = same(Xx, Xz, what);
+    check(cxm_wise_t(Xx.data(), Xz.data(), Xx.size(), fn, dt, stream()), what);
+}
+
+inline void binary(const TensorView &Xx, const TensorView &Xy, TensorView &Xz, int op, const char *what) {
+    const int dt = same(Xx, Xy, Xz, what);
+    check(cxm_binary_t(Xx.data(), Xy.data(), Xz.data(), Xx.size(), op, dt, stream()), what);
+}
+
+inline void scalar(const TensorView &Xx, float value, TensorView &Xz, int op, const char *what) {
+    const int dt = same(Xx, Xz, what);
+    check(cxm_scalar_t(Xx.data(), value, Xz.data(), Xx.size(), op, dt, stream()), what);
+}
+
+// M, K, N from |A| = M*K, |B| = K*N, |C| = M*N: M*M = |A|*|C| / |B|.
+inline bool dims(std::size_t sa, std::size_t sb, std::size_t sc, std::size_t *m, std::size_t *k, std::size_t *n) {
+    if (sa == 0 || sb == 0 || sc == 0) return false;
+    const unsigned __int128 p = static_cast<unsigned __int128>(sa) * sc;
+    if (p % sb != 0) return false;
+    const unsigned __int128 q = p / sb;
+    // integer square root of q (q < 2^128): Newton from above
+    unsigned __int128 x = q, y = (x + 1) / 2;
+    while (y < x) {
+        x = y;
+        y = (x + q / x) / 2;
+    }
+    if (x * x != q || x == 0) return false;
+    const std::size_t M = static_cast<std::size_t>(x);
+    if (sa % M != 0 || sc % M != 0) return false;
+    const std::size_t K = sa / M, N = sc / M;
+    if (static_cast<unsigned __int128>(K) * N != sb) return false;
+    *m = M;
+    *k = K;
+    *n = N;
+    return true;
+}
+
+}  // namespace nv_detail
+
+// Type/size.cpp:8-34: bytes per element (0 for Unknown).
+inline std::size_t size_of(DType t) noexcept {
+    switch (t) {
+        case DType::Int32:
+        case DType::Float32: return 4;
+        case DType::Int64:
+        case DType::Float64: return 8;
+        case DType::BFloat16:
+        case DType::Float16:
+        case DType::QInt16:
+        case DType::QUInt16: return 2;
+        case DType::QInt8:
+        case DType::QUInt8: return 1;
+        default: return 0;
     }
 }
 
@@ -134,8 +265,21 @@ struct matrix_t {
     }
 };
 
-// avx2::ScalarOp (scalar.cpp:89-119): Xz = Xx op value.
+// avx2::ScalarOp (Engine/AVX2/scalar.hpp:25-104, scalar.cpp:89-119):
+// Xz = Xx op value over TensorViews, out of place and in place, as the
+// reference declares them; views of Float32, BFloat16 or Float16 device
+// memory (the 16-bit forms widen, apply the fp32 operator and round once).
+// The pointer forms (Xx, value, Xz, N) are kept for fp32 callers.
 struct ScalarOp {
+    static void add(const TensorView &Xx, float value, TensorView &Xz) { nv_detail::scalar(Xx, value, Xz, CXM_OP_ADD, "ScalarOp::add"); }
+    static void sub(const TensorView &Xx, float value, TensorView &Xz) { nv_detail::scalar(Xx, value, Xz, CXM_OP_SUB, "ScalarOp::sub"); }
+    static void mul(const TensorView &Xx, float value, TensorView &Xz) { nv_detail::scalar(Xx, value, Xz, CXM_OP_MUL, "ScalarOp::mul"); }
+    static void div(const TensorView &Xx, float value, TensorView &Xz) { nv_detail::scalar(Xx, value, Xz, CXM_OP_DIV, "ScalarOp::div"); }
+    static void add(TensorView &Xx, float value) { nv_detail::scalar(Xx, value, Xx, CXM_OP_ADD, "ScalarOp::add"); }
+    static void sub(TensorView &Xx, float value) { nv_detail::scalar(Xx, value, Xx, CXM_OP_SUB, "ScalarOp::sub"); }
+    static void mul(TensorView &Xx, float value) { nv_detail::scalar(Xx, value, Xx, CXM_OP_MUL, "ScalarOp::mul"); }
+    static void div(TensorView &Xx, float value) { nv_detail::scalar(Xx, value, Xx, CXM_OP_DIV, "ScalarOp::div"); }
+
     static void op(const float *Xx, float v, float *Xz, std::size_t N, int code) {
         check(cxm_scalar_f32(Xx, v, Xz, N, code, stream()), "ScalarOp");
     }
@@ -145,9 +289,31 @@ struct ScalarOp {
     static void div(const float *Xx, float v, float *Xz, std::size_t N) { op(Xx, v, Xz, N, CXM_OP_DIV); }
 };
 
-// avx2::wise / nv::ElementWise (Engine/AVX2/wise.hpp:28-42,
-// Engine/CUDA/element_wise.cuh:11-27) in pointer form: Xz = fn(Xx) over N.
+// avx2::wise (Engine/AVX2/wise.hpp:27-47): Xz = fn(Xx) over TensorViews, as
+// the reference declares square..sign and both pow forms (Float32,
+// BFloat16 or Float16 device views), plus pointer forms over N fp32
+// elements; lerp, clamp and gather are pointer forms in the reference too.
 struct wise {
+    static void square(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_SQUARE, "wise::square"); }
+    static void sqrt(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_SQRT, "wise::sqrt"); }
+    static void rsqrt(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_RSQRT, "wise::rsqrt"); }
+    static void log(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_LOG, "wise::log"); }
+    static void exp(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_EXP, "wise::exp"); }
+    static void erf(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_ERF, "wise::erf"); }
+    static void sin(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_SIN, "wise::sin"); }
+    static void cos(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_COS, "wise::cos"); }
+    static void abs(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_ABS, "wise::abs"); }
+    static void neg(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_NEG, "wise::neg"); }
+    static void rcp(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_RCP, "wise::rcp"); }
+    static void inverse(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_INVERSE, "wise::inverse"); }
+    static void sign(const TensorView &Xx, TensorView &Xz) { nv_detail::unary(Xx, Xz, CXM_FN_SIGN, "wise::sign"); }
+    static void pow(const TensorView &Xx, float value, TensorView &Xz) {
+        nv_detail::scalar(Xx, value, Xz, CXM_OP_POW, "wise::pow");
+    }
+    static void pow(const TensorView &Xx, const TensorView &Xy, TensorView &Xz) {
+        nv_detail::binary(Xx, Xy, Xz, CXM_OP_POW, "wise::pow");
+    }
+
     static void fn(const float *Xx, float *Xz, std::size_t N, int code) {
         check(cxm_wise_f32(Xx, Xz, N, code, stream()), "wise");
     }
@@ -197,10 +363,6 @@ struct activation {
 };
 
 // ------------------------------------------------------------ storage
-
-// The reference's DeviceType (Memory/type.hpp:22-26) with the HIP device
-// this backend adds.
-enum class DeviceType : std::uint8_t { Unknown = 0, HOST = 1, CUDA = 2, HIP = 3 };
 
 // TensorStorage (Storage/storage.hpp:14-57) for the host and HIP devices:
 // an owning, move-only byte buffer.  HIP memory comes from the library's
@@ -291,18 +453,24 @@ private:
     DeviceType device_ = DeviceType::Unknown;
 };
 
-// A dense row-major fp32 tensor on the host or the HIP device: the part of
-// the reference's Tensor (Tensor/tensor.hpp) the operators and the autograd
-// flows need -- shape, storage, device, to(), grad, the producing flow.
+// A dense row-major tensor on the host or the HIP device: the part of the
+// reference's Tensor (Tensor/tensor.hpp:26-150) the operators and the
+// autograd flows need -- shape, dtype, storage, device, to(), view(), the
+// gradient and the producing flow.  The constructor takes the reference's
+// arguments in its order and with its defaults (Tensor/tensor.hpp:29-31:
+// Float32 on the HOST, no gradient); storage is size_of(dtype) bytes per
+// element.  The fp32 accessors (data(), host(), from_host) check the dtype.
 struct GradientFlow;
 class Tensor {
 public:
     Tensor() = default;
-    Tensor(std::vector<std::int64_t> shape, DeviceType d = DeviceType::HIP, bool requires_grad = false)
-        : shape_(std::move(shape)), requires_grad_(requires_grad) {
-        storage_ = std::make_shared<Storage>(len() * sizeof(float), d);
+    explicit Tensor(std::vector<std::int64_t> shape, DType type = DType::Float32, DeviceType d = DeviceType::HOST,
+                    bool requires_grad = false)
+        : shape_(std::move(shape)), dtype_(type), requires_grad_(requires_grad) {
+        if (size_of(type) == 0) check(CXM_E_INVALID, "Tensor: unsupported DType");
+        storage_ = std::make_shared<Storage>(len() * size_of(type), d);
     }
-    // A HIP tensor holding a copy of host data.
+    // A HIP fp32 tensor holding a copy of host data.
     static Tensor from_host(std::vector<std::int64_t> shape, const float *data, bool requires_grad = false) {
         Tensor t;
         t.shape_ = std::move(shape);
@@ -320,10 +488,31 @@ public:
     std::size_t ndim() const noexcept { return shape_.size(); }
     const std::vector<std::int64_t> &shape() const noexcept { return shape_; }
     std::int64_t dim(std::size_t i) const { return shape_.at(i); }
+    DType dtype() const noexcept { return dtype_; }
     DeviceType device() const noexcept { return storage_ ? storage_->device() : DeviceType::Unknown; }
     bool empty() const noexcept { return !storage_ || storage_->isEmpty(); }
-    float *data() { return storage_->as<float>(); }
-    const float *data() const { return storage_->as<float>(); }
+    float *data() { return get<float>(); }
+    const float *data() const { return get<float>(); }
+    std::byte *raw() noexcept { return storage_ ? storage_->raw() : nullptr; }
+    const std::byte *raw() const noexcept { return storage_ ? storage_->raw() : nullptr; }
+
+    // Tensor::get<T> (tensor.hpp:64-77): the storage as T, which must be the
+    // element type of the tensor's dtype (std::uint16_t for the 16-bit types).
+    template <class T>
+    T *get() {
+        check_type<T>();
+        return storage_->as<T>();
+    }
+    template <class T>
+    const T *get() const {
+        check_type<T>();
+        return storage_->as<T>();
+    }
+
+    // Tensor::view (tensor.hpp:124-125, tensor.cpp:183-185): a non-owning
+    // view of the elements, what the nv:: operators and the TensorView forms
+    // of ScalarOp / wise take.
+    TensorView view() const noexcept { return TensorView(storage_ ? storage_->raw() : nullptr, dtype_, device(), len()); }
 
     // Tensor::to (Tensor/tensor.cpp:151-171): moves the data to `type`.
     Tensor &to(DeviceType type) {
@@ -348,7 +537,19 @@ public:
     std::shared_ptr<Storage> storage() const { return storage_; }
 
 private:
+    template <class T>
+    void check_type() const {
+        const bool ok = (std::is_same_v<T, float> && dtype_ == DType::Float32) ||
+                        (std::is_same_v<T, double> && dtype_ == DType::Float64) ||
+                        (std::is_same_v<T, std::int32_t> && dtype_ == DType::Int32) ||
+                        (std::is_same_v<T, std::int64_t> && dtype_ == DType::Int64) ||
+                        (std::is_same_v<T, std::uint16_t> && size_of(dtype_) == 2) ||
+                        (std::is_same_v<T, std::byte>);
+        if (!ok) check(CXM_E_INVALID, "Tensor::get: element type does not match the tensor's DType");
+    }
+
     std::vector<std::int64_t> shape_;
+    DType dtype_ = DType::Float32;
     std::shared_ptr<Storage> storage_;
     std::shared_ptr<Tensor> grad_;
     std::shared_ptr<GradientFlow> flow_;

@@ -30,114 +30,9 @@
 
 namespace cortex::_fw::hip {
 
-// Type/dtype.hpp:21-33 (same values).
-enum class DType : std::uint8_t {
-    Unknown = 0,
-    Int32 = 1,
-    Int64 = 2,
-    Float32 = 3,
-    Float64 = 4,
-    BFloat16 = 5,
-    Float16 = 6,
-    QInt16 = 7,
-    QInt8 = 8,
-    QUInt16 = 9,
-    QUInt8 = 10,
-};
+// DType, TensorView and the dtype dispatch (nv_detail) are defined in
+// cortex_hip.hpp, which the pointer-form operator structs share.
 
-// Tools/view.hpp:25-83: non-owning view of `size` elements of `type`.
-class TensorView {
-public:
-    TensorView(std::byte *data, DType type, DeviceType device, std::size_t size)
-        : m_data(data), m_type(type), m_device(device), m_size(size) {}
-    TensorView(TensorView const &) = delete;
-    TensorView(TensorView &&) = delete;
-    TensorView &operator=(TensorView const &) = delete;
-    TensorView &operator=(TensorView &&) = delete;
-    ~TensorView() = default;
-
-    [[nodiscard]] std::byte *data() noexcept { return m_data; }
-    [[nodiscard]] const std::byte *data() const noexcept { return m_data; }
-    [[nodiscard]] DType dtype() const noexcept { return m_type; }
-    [[nodiscard]] DeviceType device() const noexcept { return m_device; }
-    [[nodiscard]] std::size_t size() const noexcept { return m_size; }
-
-private:
-    std::byte *m_data;
-    DType m_type;
-    DeviceType m_device;
-    std::size_t m_size;
-};
-
-namespace nv_detail {
-
-[[noreturn]] inline void fail(const char *what, const char *why) {
-    std::fprintf(stderr, "[ERROR] %s: %s\n", what, why);
-    std::exit(1);
-}
-
-// view.hpp:107-117's dispatch, as the ABI's dtype code.
-inline int code(const TensorView &v, const char *what) {
-    if (v.device() != DeviceType::HIP) fail(what, "view is not HIP device memory");
-    switch (v.dtype()) {
-        case DType::Float32: return CXM_DT_F32;
-        case DType::BFloat16: return CXM_DT_BF16;
-        case DType::Float16: return CXM_DT_F16;
-        default: fail(what, "unsupported DType");
-    }
-}
-
-inline int same(const TensorView &a, const TensorView &b, const char *what) {
-    const int c = code(a, what);
-    if (code(b, what) != c) fail(what, "operands differ in dtype");
-    if (a.size() != b.size()) fail(what, "operands differ in element count");
-    return c;
-}
-
-inline int same(const TensorView &a, const TensorView &b, const TensorView &c, const char *what) {
-    same(a, b, what);
-    return same(a, c, what);
-}
-
-inline void unary(const TensorView &Xx, TensorView &Xz, int fn, const char *what) {
-    const int dt = same(Xx, Xz, what);
-    check(cxm_wise_t(Xx.data(), Xz.data(), Xx.size(), fn, dt, stream()), what);
-}
-
-inline void binary(const TensorView &Xx, const TensorView &Xy, TensorView &Xz, int op, const char *what) {
-    const int dt = same(Xx, Xy, Xz, what);
-    check(cxm_binary_t(Xx.data(), Xy.data(), Xz.data(), Xx.size(), op, dt, stream()), what);
-}
-
-inline void scalar(const TensorView &Xx, float value, TensorView &Xz, int op, const char *what) {
-    const int dt = same(Xx, Xz, what);
-    check(cxm_scalar_t(Xx.data(), value, Xz.data(), Xx.size(), op, dt, stream()), what);
-}
-
-// M, K, N from |A| = M*K, |B| = K*N, |C| = M*N: M*M = |A|*|C| / |B|.
-inline bool dims(std::size_t sa, std::size_t sb, std::size_t sc, std::size_t *m, std::size_t *k, std::size_t *n) {
-    if (sa == 0 || sb == 0 || sc == 0) return false;
-    const unsigned __int128 p = static_cast<unsigned __int128>(sa) * sc;
-    if (p % sb != 0) return false;
-    const unsigned __int128 q = p / sb;
-    // integer square root of q (q < 2^128): Newton from above
-    unsigned __int128 x = q, y = (x + 1) / 2;
-    while (y < x) {
-        x = y;
-        y = (x + q / x) / 2;
-    }
-    if (x * x != q || x == 0) return false;
-    const std::size_t M = static_cast<std::size_t>(x);
-    if (sa % M != 0 || sc % M != 0) return false;
-    const std::size_t K = sa / M, N = sc / M;
-    if (static_cast<unsigned __int128>(K) * N != sb) return false;
-    *m = M;
-    *k = K;
-    *n = N;
-    return true;
-}
-
-}  // namespace nv_detail
 
 // nv::ElementWise (element_wise.cuh:11-27, element_wise.cu:17-181).
 struct ElementWise {

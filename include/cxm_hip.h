@@ -377,6 +377,13 @@ int cxm_softmax_xent_f32(const float *logits, const int32_t *labels, float *loss
  * the backward of avx2::relu/sigmoid/tanh (functions.hpp:372-411) that a
  * concrete GradientFlow would run. */
 int cxm_act_bwd_f32(const float *y, const float *dy, float *dx, size_t n, int act, cxm_stream_t s);
+/* Backward of reduce::sum / reduce::mean over the middle axis of [outer,
+ * dim, inner]: dx[o, d, i] = dz[o, i] (sum, mean = 0) or dz[o, i] / dim
+ * (mean = 1, the correctly rounded quotient).  dz holds outer * inner
+ * elements; dx must not overlap it.  No reference counterpart: the
+ * backward a Sum / Mean GradientFlow (Graph/flow.hpp:15-24) runs. */
+int cxm_reduce_sum_bwd_f32(const float *dz, float *dx, size_t outer, size_t dim, size_t inner, int mean,
+                           cxm_stream_t s);
 /* w -= lr * g, as matrix_t::sub(w, ScalarOp::mul(g, lr)): two roundings. */
 int cxm_sgd_f32(float *w, const float *g, float lr, size_t n, cxm_stream_t s);
 

@@ -53,7 +53,7 @@ int main() {
     // ---------------------------------------------------------- 1. storage
     {
         const std::vector<float> h = rnd(1000, 1, 1.0f);
-        hip::Tensor t({10, 100}, hip::DeviceType::HOST);
+        hip::Tensor t({10, 100}, hip::DType::Float32, hip::DeviceType::HOST);
         std::memcpy(t.data(), h.data(), h.size() * sizeof(float));
         t.to(hip::DeviceType::HIP);
         EXPECT(t.device() == hip::DeviceType::HIP, "to(HIP)");
@@ -109,7 +109,7 @@ int main() {
     hip::Tensor fB1 = hip::Tensor::from_host({(int64_t)d1}, b1.data());
     hip::Tensor fB2 = hip::Tensor::from_host({(int64_t)d2}, b2.data());
     hip::Tensor fB3 = hip::Tensor::from_host({(int64_t)d3}, b3.data());
-    hip::Tensor floss({1});
+    hip::Tensor floss({1}, hip::DType::Float32, hip::DeviceType::HIP);
     cxm_mlp3 *net = nullptr;
     hip::check(cxm_mlp3_create(&net, B, d0, d1, d2, d3), "mlp3_create");
 
@@ -148,10 +148,10 @@ int main() {
         hip::backward(y);  // seed dY = 1
         const std::vector<float> g = Wa->grad().host();
         // single path: dW = X^T 1, computed by the same GEMM
-        hip::Tensor ones({(int64_t)M, (int64_t)N});
+        hip::Tensor ones({(int64_t)M, (int64_t)N}, hip::DType::Float32, hip::DeviceType::HIP);
         const std::vector<float> one(M * N, 1.0f);
         hip::check(cxm_memcpy_h2d(ones.data(), one.data(), one.size() * 4, hip::stream()), "ones");
-        hip::Tensor single({(int64_t)K, (int64_t)N});
+        hip::Tensor single({(int64_t)K, (int64_t)N}, hip::DType::Float32, hip::DeviceType::HIP);
         hip::check(cxm_gemm_f32(Xa->data(), ones.data(), single.data(), K, M, N, 1, 0, nullptr, CXM_ACT_NONE, nullptr,
                                 hip::stream()),
                    "single");

@@ -7,6 +7,7 @@
 // and returns 1; a failed call exits(1) inside the host layer.
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <vector>
 
 #include "cortex_hip.hpp"
@@ -133,6 +134,71 @@ int main() {
         if (failures > 10) break;
     }
     for (size_t i = 0; i < gi.size(); ++i) EXPECT(hg[i] == w[gi[i]], "gather %zu", i);
+
+    // ScalarOp and wise over TensorViews (Engine/AVX2/scalar.hpp:36-104,
+    // wise.hpp:27-41), out of place and in place, on Tensors of each
+    // supported DType placed on the device (Tensor(shape, DType, DeviceType))
+    for (hip::DType t : {hip::DType::Float32, hip::DType::BFloat16, hip::DType::Float16}) {
+        const size_t L = 777;
+        std::vector<float> v(L);
+        for (size_t i = 0; i < L; ++i) v[i] = static_cast<float>(static_cast<int>(i % 31) - 15);
+        hip::Tensor a({static_cast<int64_t>(L)}, hip::DType::Float32, hip::DeviceType::HOST);
+        std::memcpy(a.data(), v.data(), L * sizeof(float));
+        a.to(hip::DeviceType::HIP);
+        hip::Tensor ta({static_cast<int64_t>(L)}, t, hip::DeviceType::HIP), tz({static_cast<int64_t>(L)}, t, hip::DeviceType::HIP);
+        EXPECT(ta.dtype() == t && ta.device() == hip::DeviceType::HIP && ta.storage()->bytes() == L * hip::size_of(t),
+               "Tensor(shape, DType, HIP) storage");
+        hip::check(cxm_convert(ta.raw(), t == hip::DType::Float32 ? CXM_DT_F32 : t == hip::DType::BFloat16 ? CXM_DT_BF16 : CXM_DT_F16,
+                               a.raw(), CXM_DT_F32, L, hip::stream()),
+                   "convert");
+        {
+            auto va = ta.view();
+            auto vz = tz.view();
+            hip::ScalarOp::mul(va, 3.0f, vz);  // out of place
+            hip::ScalarOp::add(vz, 1.0f);      // in place
+            hip::ScalarOp::sub(vz, 2.0f);
+            hip::ScalarOp::div(vz, 2.0f);
+        }
+        hip::Tensor back({static_cast<int64_t>(L)}, hip::DType::Float32, hip::DeviceType::HIP);
+        auto convert_back = [&](hip::Tensor &src) {
+            hip::check(cxm_convert(back.raw(), CXM_DT_F32, src.raw(),
+                                   t == hip::DType::Float32 ? CXM_DT_F32 : t == hip::DType::BFloat16 ? CXM_DT_BF16 : CXM_DT_F16,
+                                   L, hip::stream()),
+                       "convert back");
+            return back.host();
+        };
+        auto h = convert_back(tz);
+        for (size_t i = 0; i < L; ++i) {
+            const float want = (v[i] * 3.0f + 1.0f - 2.0f) / 2.0f;  // exact in all three types
+            EXPECT(h[i] == want, "ScalarOp over TensorView dtype %d at %zu: %f vs %f", static_cast<int>(t), i, h[i], want);
+            if (failures > 10) break;
+        }
+        {
+            auto va = ta.view();
+            auto vz = tz.view();
+            hip::wise::abs(va, vz);
+            hip::wise::square(vz, vz);
+            hip::wise::neg(vz, vz);
+        }
+        h = convert_back(tz);
+        for (size_t i = 0; i < L; ++i) {
+            EXPECT(h[i] == -(v[i] * v[i]), "wise over TensorView dtype %d at %zu", static_cast<int>(t), i);
+            if (failures > 10) break;
+        }
+        {
+            auto va = ta.view();
+            auto vz = tz.view();
+            hip::wise::pow(va, 2.0f, vz);
+            hip::wise::sign(va, va);
+        }
+        h = convert_back(tz);
+        const auto hsg = convert_back(ta);
+        for (size_t i = 0; i < L; ++i) {
+            EXPECT(std::fabs(h[i] - v[i] * v[i]) <= 1e-2f * v[i] * v[i], "wise::pow dtype %d at %zu", static_cast<int>(t), i);
+            EXPECT(hsg[i] == static_cast<float>((v[i] > 0) - (v[i] < 0)), "wise::sign in place dtype %d", static_cast<int>(t));
+            if (failures > 10) break;
+        }
+    }
 
     if (failures == 0) std::printf("ALL OK\n");
     return failures == 0 ? 0 : 1;
