@@ -58,6 +58,25 @@ struct Exchange {
 };
 int get_exchange(cxm_stream_t s, size_t rows, Exchange *x);
 
+// Tagged partial slots of the flat reductions, one region per (device,
+// stream), kept apart from the workspace scratch.  Slot i is a 64-bit word
+// (32-bit partial | tag << 32).  Each call takes a new tag (`epoch`, never
+// 0, from a host counter per region): its writers store their partials
+// with it and its reader waits for it, so a slot an earlier call left, of
+// any shape, never carries the current tag; calls on one stream are
+// ordered, so a write of an earlier call has landed before a later call
+// starts.  A graph replays its launches with the tags they were captured
+// with, so a call made under stream capture (`clear`) also has its reader
+// put every slot it consumed back to tag 0.  Zero-filled when allocated;
+// grows on demand (after a stream sync).
+struct TaggedSlots {
+    unsigned long long *slots;
+    size_t n;
+    unsigned epoch;
+    int clear;
+};
+int get_tagged(cxm_stream_t s, size_t n, TaggedSlots *t);
+
 // Polls a waiting workgroup makes for a peer's partial before it computes
 // that partial itself (cxm_exchange_wait_limit).
 unsigned exchange_wait_limit();
@@ -123,6 +142,14 @@ __device__ __forceinline__ float4 ld4(const float *p) {
 __device__ __forceinline__ float4 ld4_stream(const float *p) {
     const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
     return make_float4(v.x, v.y, v.z, v.w);
+}
+// A streaming 128-bit load at base + byte_off, with base uniform across the
+// wave and byte_off a 32-bit value: the scalar-base + 32-bit vector-offset
+// form of global_load, one address register per load where a 64-bit
+// per-lane address takes two (and the register pressure can split a batch
+// of loads).
+__device__ __forceinline__ float4 ld4_stream_at(const float *base, unsigned byte_off) {
+    return ld4_stream(reinterpret_cast<const float *>(reinterpret_cast<const char *>(base) + byte_off));
 }
 __device__ __forceinline__ void st4(float *p, float4 v) {
     *reinterpret_cast<f32x4 *>(p) = f32x4{v.x, v.y, v.z, v.w};

@@ -9,10 +9,12 @@
 // Two kernels cover every shape:
 //  * k_rows: inner == 1 (row reductions, and the flat form as one row).
 //    Each row is cut into `segs` segments; one 256-thread workgroup reduces
-//    a segment with 128-bit loads, several in flight per thread, then a DPP
-//    wave reduce and a 4-entry LDS combine.  With segs > 1 the segment
-//    results go to the workspace and the last workgroup of the row combines
-//    them in segment order.
+//    a segment with 128-bit loads (an unaligned head and a ragged tail of
+//    fewer than 4 elements each are folded in by segment 0), several in
+//    flight per thread, then a DPP wave reduce and a 4-entry LDS combine.
+//    With segs > 1 the segment results are combined in segment order: by
+//    the row's last workgroup (ticket) or, for a flat reduction, by one
+//    reader workgroup that polls tagged slots.
 //  * k_cols: inner > 1.  A workgroup owns 256 adjacent columns of one outer
 //    slice and a chunk of the reduced rows; each thread keeps one float4 of
 //    columns, the four waves take interleaved rows and meet in LDS.  Chunks
@@ -24,12 +26,18 @@
 #include "cxm_common.hpp"
 
 // Scratch of cxm_reduce_sum_noalloc_f32: ticket counters first (kCtr words
-// each), then partial results.  One copy per device, held until the process
-// ends.  Host code never passes this name to a kernel: the address of each
-// device's copy comes from hipGetSymbolAddress (fixed_scratch below).
+// each), then the tagged slots of flat reductions (64-bit words), then
+// partial results.  One copy per device, held
+// until the process ends.  Host code never passes this name to a kernel:
+// the address of each device's copy comes from hipGetSymbolAddress
+// (fixed_scratch below).
 constexpr size_t kFixedCounterBytes = size_t(1) << 20;  // 4096 counters
+constexpr size_t kFixedTagged = 2048;                    // tagged slots (the flat plan's largest split)
+constexpr size_t kFixedTaggedBytes = kFixedTagged * sizeof(unsigned long long);
 constexpr size_t kFixedPartBytes = size_t(1) << 20;
-static __device__ __align__(256) unsigned char scratch[kFixedCounterBytes + kFixedPartBytes];
+constexpr size_t kFixedZeroBytes = kFixedCounterBytes + kFixedTaggedBytes;  // cleared at set-up
+static __device__ __align__(256) unsigned char scratch[kFixedZeroBytes + kFixedPartBytes];
+static_assert(kFixedZeroBytes % 256 == 0, "partials stay 256-byte aligned");
 
 namespace cxm {
 namespace {
@@ -42,12 +50,15 @@ __global__ void k_zero_words(unsigned *p, size_t n) {
 
 constexpr int kMaxDevices = 64;
 std::atomic<unsigned char *> g_fixed[kMaxDevices];
+std::atomic<unsigned> g_fixed_epoch[kMaxDevices];  // tag of the last call on each device's static slots
 std::mutex g_fixed_mu;
 
 // Device address of the current device's `scratch`, looked up once per
-// device (with that device current) on its first use; the counters are
-// then cleared by a fill kernel on stream s.  Every kernel that takes a
-// ticket puts its counter back to zero, so they stay clear between calls.
+// device (with that device current) on its first use; the counters and the
+// tagged slots are then cleared by a fill kernel on stream s.  Every kernel
+// that takes a ticket puts its counter back to zero and every tagged slot
+// written is consumed in the same kernel, so they stay in that state
+// between calls.
 int fixed_scratch(cxm_stream_t s, unsigned char **out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -63,7 +74,7 @@ int fixed_scratch(cxm_stream_t s, unsigned char **out) {
             if (e != hipSuccess) return static_cast<int>(e);
             if (a == nullptr) return CXM_E_INVALID;
             hipLaunchKernelGGL(k_zero_words, dim3(256), dim3(256), 0, reinterpret_cast<hipStream_t>(s),
-                               static_cast<unsigned *>(a), kFixedCounterBytes / sizeof(unsigned));
+                               static_cast<unsigned *>(a), kFixedZeroBytes / sizeof(unsigned));
             e = hipGetLastError();
             if (e != hipSuccess) return static_cast<int>(e);
             p = static_cast<unsigned char *>(a);
@@ -74,19 +85,43 @@ int fixed_scratch(cxm_stream_t s, unsigned char **out) {
     return CXM_OK;
 }
 
-// Scratch for one launch: the per-stream workspace (allocated on demand),
-// or with `fixed` the static region, for callers that cannot allocate.
-int acquire(bool fixed, cxm_stream_t s, size_t counters, size_t bytes, Workspace *ws) {
-    if (!fixed) return get_workspace(s, counters, bytes, ws);
-    if (counters * kCtr * sizeof(unsigned) > kFixedCounterBytes || bytes > kFixedPartBytes)
+// Scratch of one launch: `counters` ticket counters and `bytes` of partials
+// (the per-stream workspace), or `tagged` tagged slots (their own region);
+// with `fixed`, all from the static region, for callers that cannot
+// allocate.
+struct Scratch {
+    unsigned *counters = nullptr;
+    void *part = nullptr;
+    TaggedSlots tagged{nullptr, 0, 0, 0};
+};
+int acquire(bool fixed, cxm_stream_t s, size_t counters, size_t bytes, size_t tagged, Scratch *sc) {
+    if (!fixed) {
+        if (counters || bytes) {
+            Workspace ws;
+            const int rc = get_workspace(s, counters, bytes, &ws);
+            if (rc) return rc;
+            sc->counters = ws.counters;
+            sc->part = ws.scratch;
+        }
+        if (tagged) return get_tagged(s, tagged, &sc->tagged);
+        return CXM_OK;
+    }
+    if (counters * kCtr * sizeof(unsigned) > kFixedCounterBytes || bytes > kFixedPartBytes || tagged > kFixedTagged)
         return CXM_E_TOO_LARGE;
     unsigned char *base = nullptr;
     const int rc = fixed_scratch(s, &base);
     if (rc) return rc;
-    ws->counters = reinterpret_cast<unsigned *>(base);
-    ws->counters_n = kFixedCounterBytes / (kCtr * sizeof(unsigned));
-    ws->scratch = base + kFixedCounterBytes;
-    ws->scratch_bytes = kFixedPartBytes;
+    sc->counters = reinterpret_cast<unsigned *>(base);
+    sc->part = base + kFixedZeroBytes;
+    if (tagged) {
+        int dev = 0;
+        const hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return static_cast<int>(e);
+        unsigned ep = g_fixed_epoch[dev].fetch_add(1u, std::memory_order_relaxed) + 1u;
+        if (ep == 0) ep = g_fixed_epoch[dev].fetch_add(1u, std::memory_order_relaxed) + 1u;
+        // the static slots serve any caller, captured or not: always cleared
+        sc->tagged = TaggedSlots{reinterpret_cast<unsigned long long *>(base + kFixedCounterBytes), kFixedTagged, ep, 1};
+    }
     return CXM_OK;
 }
 
@@ -161,64 +196,210 @@ __device__ __forceinline__ void fold4(typename Op::T (&acc)[4], float4 v, int ba
 // ------------------------------------------------------------------ rows
 
 constexpr unsigned kTicketGroups = 32;  // per-row ticket counters: 32 groups + 1 top
+constexpr unsigned kMaxFlatSegs = 2048;  // segments of a flat reduction (the row plan's largest split)
+constexpr size_t kMaxSeg4 = size_t(1) << 27;  // float4s of one segment (byte offsets stay below 2^31)
 
-template <class Op, bool VEC, int UNR>
-__global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, size_t dim,
-                                                 unsigned segs, size_t seg_len,
-                                                 typename Op::T *__restrict__ part,
-                                                 unsigned *__restrict__ counters, OutDesc out) {
+// A row of `dim` floats at xr (4-byte aligned) read with 128-bit loads: its
+// first h (< 4) elements come before the first 16-byte aligned address,
+// then v float4s, then t (< 4) elements.
+struct RowSplit {
+    unsigned h, t;
+    size_t v;
+};
+__device__ __forceinline__ RowSplit split_row(const float *xr, size_t dim) {
+    unsigned h = static_cast<unsigned>(((16u - (reinterpret_cast<uintptr_t>(xr) & 15u)) & 15u) / 4u);
+    if (h > dim) h = static_cast<unsigned>(dim);
+    const size_t v = (dim - h) / 4;
+    return {h, static_cast<unsigned>(dim - h - 4 * v), v};
+}
+
+// The partial of segment `seg` of one row, block-reduced (valid in every
+// thread): float4s [seg * seg4, min(seg * seg4 + seg4, v)) of the row's
+// aligned body, UNR loads in flight per thread, folded into four lane
+// accumulators in load order; segment 0 also folds the row's head and
+// tail elements.  Writers and a reader that recomputes a segment both call
+// it, so a recomputed partial has the writer's bits.  Element indices (the
+// arg operators) count from the row start; kShift operators get x - xr[0].
+template <class Op, int UNR>
+__device__ __forceinline__ typename Op::T row_segment(const float *__restrict__ xr, size_t dim, unsigned seg,
+                                                      size_t seg4, typename Op::T *lds) {
     using T = typename Op::T;
-    __shared__ T lds[kWavesPerBlock];
-    __shared__ int flag;
-
-    const unsigned b = blockIdx.x;
-    const size_t row = b / segs;
-    const unsigned seg = b - static_cast<unsigned>(row) * segs;
-    const float *__restrict__ xr = x + row * dim;
-    const size_t begin = static_cast<size_t>(seg) * seg_len;
-    const size_t end = begin + seg_len < dim ? begin + seg_len : dim;
     const int tid = threadIdx.x;
-
+    const RowSplit sp = split_row(xr, dim);
     T acc[4] = {Op::identity(), Op::identity(), Op::identity(), Op::identity()};
     float k = 0.0f;
     if constexpr (Op::kShift) k = xr[0];
     const float4 k4 = make_float4(k, k, k, k);
-    if constexpr (VEC) {
-        const size_t e4 = end / 4;
-        size_t i = begin / 4 + tid;
-        for (; i + (UNR - 1) * kBlock < e4; i += UNR * kBlock) {
-            float4 v[UNR];
+    const size_t b4 = static_cast<size_t>(seg) * seg4;
+    // the segment's float4s as a uniform base and 32-bit per-thread byte
+    // offsets (the host keeps a segment under 2^27 float4s): a 64-bit address
+    // per load costs two registers each, and the register pressure made the
+    // compiler split a batch of loads in two, each waiting for the last
+    const unsigned n4 = b4 < sp.v ? static_cast<unsigned>((b4 + seg4 < sp.v ? b4 + seg4 : sp.v) - b4) : 0u;
+    const float *__restrict__ sb = xr + sp.h + 4 * b4;
+    const int off = static_cast<int>(sp.h + 4 * b4);
+    unsigned j = tid;
+    for (; j + (UNR - 1) * kBlock < n4; j += UNR * kBlock) {
+        float4 v[UNR];
 #pragma unroll
-            for (int u = 0; u < UNR; ++u) v[u] = ld4_stream(xr + 4 * (i + u * kBlock));
+        for (int u = 0; u < UNR; ++u) v[u] = ld4_stream_at(sb, 16u * (j + u * kBlock));
 #pragma unroll
-            for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], static_cast<int>(4 * (i + u * kBlock)), 1, k4);
-        }
-        for (; i < e4; i += kBlock) fold4<Op>(acc, ld4_stream(xr + 4 * i), static_cast<int>(4 * i), 1, k4);
-    } else {
-        for (size_t i = begin + tid; i < end; i += kBlock) {
-            float v = xr[i];
-            if constexpr (Op::kShift) v = v - k;
-            acc[0] = Op::accum(acc[0], v, static_cast<int>(i));
+        for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], off + static_cast<int>(4 * (j + u * kBlock)), 1, k4);
+    }
+    for (; j < n4; j += kBlock) fold4<Op>(acc, ld4_stream_at(sb, 16u * j), off + static_cast<int>(4 * j), 1, k4);
+    if (seg == 0) {
+        // head elements to threads 0..h-1, tail elements to threads 4..4+t-1
+        int i = -1;
+        if (tid < static_cast<int>(sp.h)) i = tid;
+        else if (tid >= 4 && tid < 4 + static_cast<int>(sp.t)) i = static_cast<int>(sp.h + 4 * sp.v) + (tid - 4);
+        if (i >= 0) {
+            float e = xr[i];
+            if constexpr (Op::kShift) e = e - k;
+            acc[0] = Op::accum(acc[0], e, i);
         }
     }
     T r = Op::combine(Op::combine(acc[0], acc[1]), Op::combine(acc[2], acc[3]));
-    r = block_reduce<Op, kBlock>(r, lds);
+    return block_reduce<Op, kBlock>(r, lds);
+}
 
-    if (segs == 1) {
-        if (tid == 0) write_out<Op>(out, row, r);
+// Reductions over the last axis: workgroup b reduces segment b % segs of
+// row b / segs.  MODE 0: one segment per row, written out directly.
+// MODE 1: segment partials to `part`; the last workgroup of a row (integer
+// ticket: one counter per row up to 32 segments, two levels beyond)
+// combines them in segment order.  MODE 2 (one row, 32-bit partials, at
+// most kMaxFlatSegs segments): the writers store tagged partials and exit,
+// with no atomics; one extra workgroup (the last of the grid, dispatched
+// after every writer) waits for each tag with at most poll_limit polls,
+// recomputes any partial it did not see in time from the input with the
+// writer's arithmetic, and combines them in segment order.  A ticket with
+// every workgroup of a 2048-segment row arriving on the counters at the end
+// serialised there (about 10 ns per atomic on one address): measured on
+// gfx950 for a 64 MiB flat sum, two-level ticket 13.1 us, one reader
+// polling tagged slots 12.0-12.3 us, streaming alone 11.2 us.  Both combine
+// the same partials in the same order, so their results are bit-identical.
+template <class Op, int UNR, int MODE>
+__global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, size_t dim, unsigned segs, size_t seg4,
+                                                 typename Op::T *__restrict__ part, unsigned *__restrict__ counters,
+                                                 unsigned long long *__restrict__ slots, unsigned epoch, int clear,
+                                                 unsigned poll_limit, OutDesc out) {
+    using T = typename Op::T;
+    __shared__ T lds[kWavesPerBlock];
+    __shared__ int flag;
+    const int tid = threadIdx.x;
+
+    if constexpr (MODE == 2) {
+        static_assert(sizeof(T) == 4, "tagged slots carry 32-bit partials");
+        constexpr int IT = kMaxFlatSegs / kBlock;
+        if (blockIdx.x == segs) {  // the reader
+            // The first loads are unconditional (the slot regions hold at
+            // least kMaxFlatSegs entries): a load in a branch makes the
+            // compiler wait for it at the branch's end, serialising the
+            // round trips.  Every writer was dispatched before
+            // this workgroup and none waits for anything, so each tag
+            // arrives; the poll limit only bounds the wait regardless.
+            __shared__ unsigned lmiss[kBlock];
+            unsigned long long v[IT];
+            T val[IT];
+#pragma unroll
+            for (int k = 0; k < IT; ++k)
+                v[k] = __hip_atomic_load(slots + tid + k * kBlock, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // then, per slot not yet tagged, in segment order (segments finish
+            // roughly in dispatch order): one 8-byte load per thread per round,
+            // so the polling traffic stays negligible
+            unsigned miss = 0;
+#pragma unroll
+            for (int k = 0; k < IT; ++k) {
+                const unsigned i = tid + k * kBlock;
+                val[k] = Op::identity();
+                if (i < segs) {
+                    unsigned long long w = v[k];
+                    unsigned polls = 0;
+                    while (static_cast<unsigned>(w >> 32) != epoch && polls < poll_limit) {
+                        ++polls;
+                        __builtin_amdgcn_s_sleep(1);
+                        w = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                    if (static_cast<unsigned>(w >> 32) == epoch) {
+                        val[k] = __builtin_bit_cast(T, static_cast<unsigned>(w));
+                        if (clear) __hip_atomic_store(slots + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    } else {
+                        miss |= 1u << k;
+                    }
+                }
+            }
+            // segments not seen in time (none, unless the wait limit is
+            // small): recomputed by the whole workgroup with one load in
+            // flight per thread -- the writer's fold order (each thread folds
+            // its float4s in index order whatever the unroll), so its bits
+            if (__syncthreads_or(miss != 0u)) {
+                lmiss[tid] = miss;
+                __syncthreads();
+                for (unsigned i = 0; i < segs; ++i) {
+                    const unsigned t = i % kBlock, k = i / kBlock;
+                    if (!((lmiss[t] >> k) & 1u)) continue;  // uniform: every thread reads the same word
+                    const T r = row_segment<Op, 1>(x, dim, i, seg4, lds);
+                    if (tid == static_cast<int>(t)) {
+#pragma unroll
+                        for (int q = 0; q < IT; ++q)
+                            if (q == static_cast<int>(k)) val[q] = r;
+                    }
+                }
+            }
+            T a = Op::identity();
+#pragma unroll
+            for (int k = 0; k < IT; ++k)
+                if (tid + k * kBlock < segs) a = Op::combine(a, val[k]);
+            a = block_reduce<Op, kBlock>(a, lds);
+            if (tid == 0) write_out<Op>(out, 0, a);
+            return;
+        }
+        // a writer
+        const T r = row_segment<Op, UNR>(x, dim, blockIdx.x, seg4, lds);
+        if (tid == 0) {
+            const unsigned long long v = (static_cast<unsigned long long>(epoch) << 32) | __builtin_bit_cast(unsigned, r);
+            __hip_atomic_store(slots + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         return;
+    } else {
+        const unsigned b = blockIdx.x;
+        const size_t row = b / segs;
+        const unsigned seg = b - static_cast<unsigned>(row) * segs;
+        const T r = row_segment<Op, UNR>(x + row * dim, dim, seg, seg4, lds);
+        if constexpr (MODE == 0) {
+            if (tid == 0) write_out<Op>(out, row, r);
+        } else {
+            if (tid == 0) st_dev(&part[row * segs + seg], r);
+            const bool last = segs <= kTicketGroups
+                                  ? last_block_ticket(ctr(counters, row), segs, &flag)
+                                  : last_block_ticket2<kTicketGroups>(ctr(counters, row * (kTicketGroups + 1)),
+                                                                      segs, seg, &flag);
+            if (!last) return;
+            const unsigned mine = tid < static_cast<int>(segs) ? (segs - tid + kBlock - 1) / kBlock : 0;
+            T a = combine_partials<Op>(part + row * segs + tid, mine, kBlock, Op::identity());
+            a = block_reduce<Op, kBlock>(a, lds);
+            if (tid == 0) write_out<Op>(out, row, a);
+        }
     }
-    if (tid == 0) st_dev(&part[row * segs + seg], r);
-    // one ticket per row while segments are few, two-level beyond that
-    const bool last = segs <= kTicketGroups
-                          ? last_block_ticket(ctr(counters, row), segs, &flag)
-                          : last_block_ticket2<kTicketGroups>(ctr(counters, row * (kTicketGroups + 1)),
-                                                              segs, seg, &flag);
-    if (!last) return;
-    const unsigned mine = tid < static_cast<int>(segs) ? (segs - tid + kBlock - 1) / kBlock : 0;
-    T a = combine_partials<Op>(part + row * segs + tid, mine, kBlock, Op::identity());
-    a = block_reduce<Op, kBlock>(a, lds);
-    if (tid == 0) write_out<Op>(out, row, a);
+}
+
+// Rows whose base is not 4-byte aligned: element by element, one
+// workgroup per row.
+template <class Op>
+__global__ __launch_bounds__(kBlock) void k_rows_bytes(const float *__restrict__ x, size_t dim, OutDesc out) {
+    using T = typename Op::T;
+    __shared__ T lds[kWavesPerBlock];
+    const size_t row = blockIdx.x;
+    const float *xr = x + row * dim;
+    float k = 0.0f;
+    if constexpr (Op::kShift) k = xr[0];
+    T acc = Op::identity();
+    for (size_t i = threadIdx.x; i < dim; i += kBlock) {
+        float e = xr[i];
+        if constexpr (Op::kShift) e = e - k;
+        acc = Op::accum(acc, e, static_cast<int>(i));
+    }
+    acc = block_reduce<Op, kBlock>(acc, lds);
+    if (threadIdx.x == 0) write_out<Op>(out, row, acc);
 }
 
 // ------------------------------------------------------------------ cols
@@ -229,30 +410,26 @@ constexpr int kColTile = 256;  // columns per workgroup
 // one float4 per lane and wave w takes rows r0+w, r0+w+NW, ...; scalar
 // path: thread t owns column t%256 and rows r0+t/256, step NW/4.  The
 // per-slot results meet in LDS and threads 0..255 combine them in slot
-// order.  Workgroup b -> (tile, chunk, outer slice): with tile_major the
-// chunks of one tile are adjacent in launch order (its combine runs while
-// later tiles still stream), else the tiles of one row chunk are adjacent.
-template <class Op, bool VEC, int UNR, int NW>
+// order.  Workgroup b -> (chunk, tile, outer slice), chunk fastest: the
+// chunks of one tile are adjacent in launch order, so its combine runs
+// while later tiles still stream.
+template <class Op, bool VEC, int UNR, int NW, bool FAST = false>
 __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x, size_t dim,
                                                      size_t inner, unsigned ntiles, unsigned chunks,
-                                                     size_t rows_per_chunk, int tile_major,
-                                                     typename Op::T *__restrict__ part,
+                                                     size_t rows_per_chunk, typename Op::T *__restrict__ part,
                                                      unsigned *__restrict__ counters, OutDesc out) {
     using T = typename Op::T;
     constexpr int NSLOT = VEC ? NW : NW / 4;
     __shared__ T lds[NSLOT][kColTile];
     __shared__ int flag;
 
+    // 32-bit divisions: the grid has fewer than 2^31 workgroups (a 64-bit
+    // division is a long software sequence ahead of every thread's first load)
     const unsigned b = blockIdx.x;
-    unsigned tile, chunk;
-    if (tile_major) {
-        chunk = b % chunks;
-        tile = (b / chunks) % ntiles;
-    } else {
-        tile = b % ntiles;
-        chunk = (b / ntiles) % chunks;
-    }
-    const size_t o = b / (static_cast<size_t>(ntiles) * chunks);
+    const unsigned q = b / chunks;
+    const unsigned chunk = b - q * chunks;
+    const unsigned tile = q % ntiles;
+    const size_t o = q / ntiles;
     const int tid = threadIdx.x;
     const float *__restrict__ xo = x + o * dim * inner;
     const size_t r0 = chunk * rows_per_chunk;
@@ -263,19 +440,46 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
         const int w = tid / kWave;
         const size_t col = static_cast<size_t>(tile) * kColTile + lane * 4;
         T acc[4] = {Op::identity(), Op::identity(), Op::identity(), Op::identity()};
-        if (col < inner) {
+        // FAST (whole tiles, a chunk under 2^31 bytes): no column bound to
+        // branch on, so every operand is at hand from the start -- behind
+        // the branch the compiler fetched the input pointer in a second
+        // round of kernel-argument loads after the index arithmetic, a
+        // scalar-cache miss in every workgroup (one per CU here)
+        if (FAST || col < inner) {
             const float *__restrict__ xc = xo + col;
             float4 k4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             if constexpr (Op::kShift) k4 = ld4(xc);
-            size_t r = r0 + w;
-            for (; r + (UNR - 1) * NW < r1; r += UNR * NW) {
-                float4 v[UNR];
+            if constexpr (FAST) {
+                // the chunk as a uniform base and 32-bit byte offsets: one
+                // address register per load instead of two
+                const float *__restrict__ cb = xo + r0 * inner + static_cast<size_t>(tile) * kColTile;
+                const unsigned rowb = static_cast<unsigned>(inner * sizeof(float)), nr = static_cast<unsigned>(r1 - r0);
+                const unsigned c16 = static_cast<unsigned>(lane * 16);
+                unsigned r = w;
+                for (; r + (UNR - 1) * NW < nr; r += UNR * NW) {
+                    float4 v[UNR];
 #pragma unroll
-                for (int u = 0; u < UNR; ++u) v[u] = ld4_stream(xc + (r + u * NW) * inner);
+                    for (int u = 0; u < UNR; ++u) v[u] = ld4_stream_at(cb, (r + u * NW) * rowb + c16);
+                    // all UNR loads leave before any is folded: left alone, the
+                    // scheduler interleaved the folds to stay at 64 registers
+                    // and kept 5-6 loads in flight (one 16-wave workgroup per
+                    // CU leaves room for 128); streaming 12.1 -> 11.8 us at C2
+                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], static_cast<int>(r + u * NW), 0, k4);
+                    for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], static_cast<int>(r0 + r + u * NW), 0, k4);
+                }
+                for (; r < nr; r += NW) fold4<Op>(acc, ld4_stream_at(cb, r * rowb + c16), static_cast<int>(r0 + r), 0, k4);
+            } else {
+                size_t r = r0 + w;
+                for (; r + (UNR - 1) * NW < r1; r += UNR * NW) {
+                    float4 v[UNR];
+#pragma unroll
+                    for (int u = 0; u < UNR; ++u) v[u] = ld4_stream(xc + (r + u * NW) * inner);
+#pragma unroll
+                    for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], static_cast<int>(r + u * NW), 0, k4);
+                }
+                for (; r < r1; r += NW) fold4<Op>(acc, ld4_stream(xc + r * inner), static_cast<int>(r), 0, k4);
             }
-            for (; r < r1; r += NW) fold4<Op>(acc, ld4_stream(xc + r * inner), static_cast<int>(r), 0, k4);
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) lds[w][lane * 4 + c] = acc[c];
@@ -304,7 +508,7 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
     }
     const size_t col = static_cast<size_t>(tile) * kColTile + tid;
     if (chunks == 1) {
-        if (owner && col < inner) write_out<Op>(out, o * inner + col, mine);
+        if (owner && (FAST || col < inner)) write_out<Op>(out, o * inner + col, mine);
         return;
     }
     const size_t slot = (o * ntiles + tile) * chunks;
@@ -312,7 +516,7 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
     if (!last_block_ticket(ctr(counters, o * ntiles + tile), chunks, &flag)) return;
     if (owner) {
         const T a = combine_partials<Op>(part + slot * kColTile + tid, chunks, kColTile, Op::identity());
-        if (col < inner) write_out<Op>(out, o * inner + col, a);
+        if (FAST || col < inner) write_out<Op>(out, o * inner + col, a);
     }
 }
 
@@ -322,61 +526,78 @@ __global__ void k_fill_f32(float *z, float v) { *z = v; }
 
 constexpr unsigned kTargetBlocks = 2048;
 
-template <class Op, int UNRV = 8>
+template <class Op, int UNR, int MODE>
+void launch_rows(unsigned nb, hipStream_t hs, const float *x, size_t dim, unsigned segs, size_t seg4,
+                 typename Op::T *part, unsigned *counters, const TaggedSlots &tg, OutDesc out) {
+    hipLaunchKernelGGL((k_rows<Op, UNR, MODE>), dim3(nb), dim3(kBlock), 0, hs, x, dim, segs, seg4, part, counters,
+                       tg.slots, tg.epoch, tg.clear, exchange_wait_limit(), out);
+}
+
+// Row plan: each row cut into `segs` segments of seg4 float4s (a multiple
+// of 256, i.e. 1024 floats), so that the grid has about kTargetBlocks
+// workgroups when rows are few.
+template <class Op>
 int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t s, bool fixed = false) {
     using T = typename Op::T;
     hipStream_t hs = reinterpret_cast<hipStream_t>(s);
-    const bool vec = aligned16(x) && dim % 4 == 0;
-    // Segment length: a multiple of 256 threads x 4 floats, split so that the
-    // grid has about kTargetBlocks workgroups when there are few rows.
+    if ((reinterpret_cast<uintptr_t>(x) & 3u) != 0) {
+        if (rows > 0x7fffffffu) return CXM_E_TOO_LARGE;
+        hipLaunchKernelGGL(k_rows_bytes<Op>, dim3(static_cast<unsigned>(rows)), dim3(kBlock), 0, hs, x, dim, out);
+        return launch_status();
+    }
+    const size_t v4 = (dim + 3) / 4;  // float4s of the longest aligned body (rounded up; a row has at most this many)
     size_t segs = 1;
     if (rows < kTargetBlocks) {
         const size_t want = (kTargetBlocks + rows - 1) / rows;
-        const size_t max_segs = (dim + 1023) / 1024;
+        const size_t max_segs = (v4 + 255) / 256;
         segs = want < max_segs ? want : max_segs;
         if (segs == 0) segs = 1;
     }
-    size_t seg_len = (dim + segs - 1) / segs;
-    seg_len = (seg_len + 1023) / 1024 * 1024;
-    segs = seg_len ? (dim + seg_len - 1) / seg_len : 1;
+    size_t seg4 = (v4 + segs - 1) / segs;
+    seg4 = (seg4 + 255) / 256 * 256;
+    if (seg4 == 0) seg4 = 256;
+    if (seg4 > kMaxSeg4) seg4 = kMaxSeg4;  // 32-bit byte offsets within a segment
+    segs = (v4 + seg4 - 1) / seg4;
     if (segs == 0) segs = 1;
     const size_t blocks = rows * segs;
     if (blocks > 0x7fffffffu) return CXM_E_TOO_LARGE;
-
+    const unsigned nb = static_cast<unsigned>(blocks), sg = static_cast<unsigned>(segs);
+    const bool unr8 = seg4 / kBlock >= 8;  // float4 loads per thread per segment
     T *part = nullptr;
     unsigned *counters = nullptr;
-    if (segs > 1) {
-        Workspace ws;
+    TaggedSlots tg{nullptr, 0, 0, 0};
+    const int mode = segs == 1 ? 0 : (rows == 1 && sizeof(T) == 4 && segs <= kMaxFlatSegs ? 2 : 1);
+    if (mode == 1) {
         const size_t nctr = segs <= kTicketGroups ? rows : rows * (kTicketGroups + 1);
-        int rc = acquire(fixed, s, nctr, rows * segs * sizeof(T), &ws);
+        Scratch sc;
+        int rc = acquire(fixed, s, nctr, rows * segs * sizeof(T), 0, &sc);
         if (rc) return rc;
-        part = static_cast<T *>(ws.scratch);
-        counters = ws.counters;
+        part = static_cast<T *>(sc.part);
+        counters = sc.counters;
+    } else if (mode == 2) {
+        Scratch sc;
+        int rc = acquire(fixed, s, 0, 0, segs, &sc);
+        if (rc) return rc;
+        tg = sc.tagged;
     }
-    const unsigned nb = static_cast<unsigned>(blocks);
-    const size_t per_thread = seg_len / (4 * kBlock);  // float4 loads per thread
-    if (vec && per_thread >= UNRV)
-        hipLaunchKernelGGL((k_rows<Op, true, UNRV>), dim3(nb), dim3(kBlock), 0, hs, x, dim,
-                           static_cast<unsigned>(segs), seg_len, part, counters, out);
-    else if (vec)
-        hipLaunchKernelGGL((k_rows<Op, true, 4>), dim3(nb), dim3(kBlock), 0, hs, x, dim,
-                           static_cast<unsigned>(segs), seg_len, part, counters, out);
-    else
-        hipLaunchKernelGGL((k_rows<Op, false, 1>), dim3(nb), dim3(kBlock), 0, hs, x, dim,
-                           static_cast<unsigned>(segs), seg_len, part, counters, out);
+    const unsigned grid = mode == 2 ? nb + 1 : nb;
+#define CXM_ROWS(U, M) launch_rows<Op, U, M>(grid, hs, x, dim, sg, seg4, part, counters, tg, out)
+    if (mode == 0) { if (unr8) CXM_ROWS(8, 0); else CXM_ROWS(4, 0); }
+    else if (mode == 1) { if (unr8) CXM_ROWS(8, 1); else CXM_ROWS(4, 1); }
+    else if constexpr (sizeof(T) == 4) { if (unr8) CXM_ROWS(8, 2); else CXM_ROWS(4, 2); }
+#undef CXM_ROWS
     return launch_status();
 }
 
 struct ColPlan {
     int nw;          // waves per workgroup (4 or 16)
     size_t chunks;   // row chunks per column tile
-    int tile_major;  // launch order
 };
 
 // Default plan: 16-wave workgroups and about one workgroup per CU in
 // total (few chunks, so the last-workgroup combine reads few partials).
 ColPlan col_plan(size_t tiles, size_t dim) {
-    ColPlan p{16, 1, 1};
+    ColPlan p{16, 1};
     if (tiles < 256) {
         size_t want = (256 + tiles - 1) / tiles;
         const size_t max_chunks = (dim + 63) / 64;  // >= 4 rows per wave
@@ -405,17 +626,25 @@ int run_cols_plan(const float *x, size_t outer, size_t dim, size_t inner, OutDes
     T *part = nullptr;
     unsigned *counters = nullptr;
     if (chunks > 1) {
-        Workspace ws;
-        int rc = acquire(fixed, s, tiles, tiles * chunks * kColTile * sizeof(T), &ws);
+        Scratch sc;
+        int rc = acquire(fixed, s, tiles, tiles * chunks * kColTile * sizeof(T), 0, &sc);
         if (rc) return rc;
-        part = static_cast<T *>(ws.scratch);
-        counters = ws.counters;
+        part = static_cast<T *>(sc.part);
+        counters = sc.counters;
     }
     const unsigned nb = static_cast<unsigned>(blocks);
     const unsigned nt = static_cast<unsigned>(ntiles), nc = static_cast<unsigned>(chunks);
-#define CXM_COLS(VEC_, UNR_, NW_)                                                                   \
-    hipLaunchKernelGGL((k_cols<Op, VEC_, UNR_, NW_>), dim3(nb), dim3(NW_ * kWave), 0, hs, x, dim, inner, \
-                       nt, nc, rpc, plan.tile_major, part, counters, out)
+    // whole tiles and 32-bit byte offsets within a chunk (under 2^31 bytes)
+    const bool fast = inner % kColTile == 0 && (rpc * inner + kColTile) * sizeof(float) < (size_t(1) << 31);
+#define CXM_COLS(VEC_, UNR_, NW_)                                                                              \
+    do {                                                                                                       \
+        if (VEC_ && fast)                                                                                      \
+            hipLaunchKernelGGL((k_cols<Op, VEC_, UNR_, NW_, true>), dim3(nb), dim3(NW_ * kWave), 0, hs, x, dim, \
+                               inner, nt, nc, rpc, part, counters, out);                                       \
+        else                                                                                                   \
+            hipLaunchKernelGGL((k_cols<Op, VEC_, UNR_, NW_>), dim3(nb), dim3(NW_ * kWave), 0, hs, x, dim, inner, \
+                               nt, nc, rpc, part, counters, out);                                              \
+    } while (0)
     if (plan.nw == 16) {
         // With a multiple of 16 rows per wave, all 16 loads of a batch are in
         // flight together (C2's column reductions: 13.4 against 13.8 us with

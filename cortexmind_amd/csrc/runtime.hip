@@ -29,12 +29,16 @@ struct WsEntry {
     size_t scratch_bytes = 0;
     void *xbase = nullptr;  // exchange region (never shared with other kernels' scratch)
     size_t xrows = 0;
+    void *tbase = nullptr;  // tagged partial slots (never shared either)
+    size_t tslots = 0;
+    unsigned tepoch = 0;    // tag of the last call that used them
 };
 
 void free_entry(WsEntry &w) {
     if (w.base) (void)hipFree(w.base);
     if (w.xbase) (void)hipFree(w.xbase);
-    w.base = w.xbase = nullptr;
+    if (w.tbase) (void)hipFree(w.tbase);
+    w.base = w.xbase = w.tbase = nullptr;
 }
 
 std::atomic<unsigned> g_xwait{1u << 16};
@@ -119,6 +123,47 @@ int get_exchange(cxm_stream_t s, size_t rows, Exchange *x) {
     }
     x->hdr = static_cast<unsigned *>(w.xbase);
     x->slots = reinterpret_cast<unsigned long long *>(static_cast<unsigned *>(w.xbase) + w.xrows * kCtr);
+    return CXM_OK;
+}
+
+int get_tagged(cxm_stream_t s, size_t n, TaggedSlots *t) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return st(e);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(reinterpret_cast<hipStream_t>(s), &cap);
+    if (e != hipSuccess) return st(e);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    WsEntry &w = g_ws[{dev, s}];
+    if (w.tbase == nullptr || w.tslots < n) {
+        size_t nn = n < 4096 ? 4096 : n;
+        if (w.tslots > nn) nn = w.tslots;
+        if (w.tbase != nullptr) {
+            e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(s));
+            if (e != hipSuccess) return st(e);
+            e = hipFree(w.tbase);
+            w.tbase = nullptr;
+            w.tslots = 0;
+            if (e != hipSuccess) return st(e);
+        }
+        const size_t bytes = nn * sizeof(unsigned long long);
+        void *p = nullptr;
+        e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) return st(e);
+        // all-zero: every slot tagged 0, a tag no call uses
+        e = hipMemsetAsync(p, 0, bytes, reinterpret_cast<hipStream_t>(s));
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            return st(e);
+        }
+        w.tbase = p;
+        w.tslots = nn;
+    }
+    if (++w.tepoch == 0) w.tepoch = 1;
+    t->slots = static_cast<unsigned long long *>(w.tbase);
+    t->n = w.tslots;
+    t->epoch = w.tepoch;
+    t->clear = cap != hipStreamCaptureStatusNone ? 1 : 0;
     return CXM_OK;
 }
 
@@ -285,6 +330,7 @@ int cxm_release_workspaces(void) {
         hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(kv.first.second));
         if (e == hipSuccess && kv.second.base) e = hipFree(kv.second.base);
         if (e == hipSuccess && kv.second.xbase) e = hipFree(kv.second.xbase);
+        if (e == hipSuccess && kv.second.tbase) e = hipFree(kv.second.tbase);
         if (e != hipSuccess && rc == CXM_OK) rc = st(e);
     }
     g_ws.clear();

@@ -310,8 +310,10 @@ int cxm_softmax_bwd_f32(const float *y, const float *dy, float *dx, size_t rows,
                         int log_mode, cxm_stream_t s);
 /* Kernels whose workgroups exchange partial results through device memory
  * -- the one-pass softmax of rows of 4097..524288 columns (up to 8192
- * rows) -- let a workgroup wait at most `polls` polls (default 65536) for a
- * peer's partial before it computes that partial from the input itself.  Either way the result is the same bit
+ * rows), and the flat sum / mean / max / min / norm1 / norm2 over more than
+ * 1024 elements -- let a workgroup wait at most `polls` polls (default
+ * 65536) for a peer's partial before it computes that partial from the
+ * input itself.  Either way the result is the same bit
  * for bit; 0 makes every waiting workgroup compute (for tests of that
  * path).  Process-wide; *previous (if not NULL) gets the old value.  No
  * reference counterpart. */

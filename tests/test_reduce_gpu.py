@@ -194,3 +194,56 @@ def test_engine_mirror_names(hip, orc):
     assert np.array_equal(dz.numpy(), orc.reduce_axis("max", x, 3, 50, 8))
     engine.reduce.sum(dx, dz, x.size)
     assert abs(dz.numpy()[0] - np.sum(x.astype(np.float64))) <= SUM_TOL * np.abs(x).sum()
+
+
+def _wait_limit(polls):
+    old = ctypes.c_uint(0)
+    call("cxm_exchange_wait_limit", polls, ctypes.byref(old))
+    return old.value
+
+
+@pytest.mark.parametrize("n", [4096 * 4096, (1 << 20) + 3, 1000003])
+@pytest.mark.parametrize("op", ["sum", "mean", "max", "min", "norm1", "norm2"])
+def test_flat_recompute_is_bit_identical(hip, orc, n, op):
+    """Flat reductions with 32-bit partials combine them in one reader
+    workgroup that waits for tagged slots; a partial it does not see within
+    the wait limit is recomputed from the input with the writer's arithmetic.
+    Forcing that for every segment (limit 0) gives the same bits."""
+    x = SplitMix64(0xF1A7 + n).uniform((n,), -1.0, 1.0)
+    normal = gpu_reduce(op, x, (n,))
+    old = _wait_limit(0)
+    try:
+        forced = gpu_reduce(op, x, (n,))
+    finally:
+        _wait_limit(old)
+    assert normal.tobytes() == forced.tobytes()
+    ref = orc.reduce_flat(op, x)
+    if op in ("max", "min"):
+        assert normal.tobytes() == ref.tobytes()
+    else:
+        assert abs(float(normal[0]) - float(ref[0])) <= SUM_TOL * max(float(np.abs(x).sum()), 1e-30)
+
+
+def test_flat_slot_state_across_shapes(hip, orc):
+    """Flat reductions of different lengths (different segment counts over
+    the same tagged slots), interleaved with row, column and segmented-row
+    reductions on the same stream, each checked against the oracle: no call
+    reads a partial an earlier call left behind."""
+    g = SplitMix64(0x51075)
+    seq = [(1 << 24,), (100003,), (3, 50000, 1), (1 << 24,), (5000,), (1, 4096, 4096), ((1 << 22) + 1,),
+           (1 << 24,), (777,), (1 << 21,)]
+    for sizes in seq:
+        x = g.uniform(sizes if len(sizes) > 1 else sizes[0], -1.0, 1.0)
+        check("sum", x, sizes, orc)
+        check("max", x, sizes, orc)
+
+
+@pytest.mark.parametrize("off", [1, 2, 3])
+@pytest.mark.parametrize("sizes", [((1 << 22) + 3,), (3, 100003, 1), (64, 4097, 1), (2, 5, 1)])
+@pytest.mark.parametrize("op", ["sum", "max", "argmax"])
+def test_unaligned_ragged_rows(hip, orc, off, sizes, op):
+    """Row bases off 16-byte alignment and lengths not a multiple of 4: each
+    row's head (before its first aligned float4) and tail are folded in by
+    its first segment, the body still takes 128-bit loads."""
+    x = SplitMix64(off * 7919 + sum(sizes)).normal(sizes if len(sizes) > 1 else sizes[0], 0.0, 2.0)
+    check(op, x, sizes, orc, ptr_offset_floats=off)

@@ -62,23 +62,29 @@ def _free_bytes():
 
 def test_noalloc_allocates_nothing(hip):
     """Device free memory does not move across noalloc calls on a fresh
-    stream, while the allocating entry point on another fresh stream takes
-    its workspace (at least 8 MiB), which shows the measure can see it."""
+    stream (a flat sum, whose segments meet in tagged slots, and a
+    segmented row sum, whose segments meet through a ticket), while the
+    allocating entry point on another fresh stream takes its workspace for
+    the segmented row sum (at least 8 MiB), which shows the measure can see
+    an allocation."""
     from cortexmind_amd.device import Stream
 
     n = 1 << 22
     x = SplitMix64(9).uniform((n,), -1.0, 1.0)
     dx = DeviceArray.from_numpy(x)
-    dz = DeviceArray((1,), np.float32)
+    dz = DeviceArray((64,), np.float32)
+    rows = (4, n // 4, 1)  # a few long rows: several segments per row, combined by ticket
     s1, s2 = Stream(), Stream()
-    call("cxm_reduce_sum_noalloc_f32", dx.ptr, dz.ptr, 1, n, 1, s1.handle)  # set-up on this device
+    for sizes in [(1, n, 1), rows]:  # set-up on this device
+        call("cxm_reduce_sum_noalloc_f32", dx.ptr, dz.ptr, *sizes, s1.handle)
     s1.sync()
     f0 = _free_bytes()
     for _ in range(3):
-        call("cxm_reduce_sum_noalloc_f32", dx.ptr, dz.ptr, 1, n, 1, s1.handle)
+        for sizes in [(1, n, 1), rows]:
+            call("cxm_reduce_sum_noalloc_f32", dx.ptr, dz.ptr, *sizes, s1.handle)
     s1.sync()
     f1 = _free_bytes()
-    call("cxm_reduce_sum_f32", dx.ptr, dz.ptr, 1, n, 1, s2.handle)
+    call("cxm_reduce_sum_f32", dx.ptr, dz.ptr, *rows, s2.handle)
     s2.sync()
     f2 = _free_bytes()
     assert f1 == f0, (f0, f1)
