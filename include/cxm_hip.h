@@ -161,13 +161,13 @@ int cxm_reduce_argmax_f32(const float *x, int32_t *z, size_t outer, size_t dim, 
 /* cxm_reduce_sum_f32 for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference.  Same arguments, kernels and bits as
- * cxm_reduce_sum_f32 (the flat sum is (1, n, 1)); its partial sums and
- * ticket counters live in a static 2 MiB region per device (1 MiB of
- * counters, 1 MiB of partials) instead of the per-stream workspace, and it
- * calls no hipMalloc or hipFree.  That region covers every shape the
- * reduction plan produces; a shape needing more gives CXM_E_TOO_LARGE.  The
- * first call on a device looks the region up and clears its counters with a
- * kernel on stream s.  All calls on one device share the region: two calls
+ * cxm_reduce_sum_f32 (the flat sum is (1, n, 1)); its partial sums, ticket
+ * counters and tagged slots live in a static region per device (1 MiB of
+ * counters, 16 KiB of slots, 1 MiB of partials) instead of the per-stream
+ * workspace, and it calls no hipMalloc or hipFree.  That region covers every
+ * shape the reduction plan produces; a shape needing more gives
+ * CXM_E_TOO_LARGE.  The first call on a device looks the region up and
+ * clears its counters and slots with a kernel on stream s.  All calls on one device share the region: two calls
  * that overlap in time on one device (different streams, or host threads)
  * race and must be serialised by the caller. */
 int cxm_reduce_sum_noalloc_f32(const float *x, float *z, size_t outer, size_t dim, size_t inner,
