@@ -1,0 +1,95 @@
+"""Reductions captured into a HIP graph and replayed.
+
+A flat reduction's writers tag their partials with a per-call tag that a
+graph replays unchanged, so a call made under stream capture has its reader
+clear every slot it consumed; the no-allocation entry point (meant for such
+callers) always does.  Each replay here runs on new input data, with eager
+reductions of other shapes on the same stream between the replays, and must
+give the bits an eager call gives on that data.  The captured launches
+record kernels only: the regions they use exist before capture starts (an
+eager call first), so no allocation or memset is captured."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from cortexmind_amd._lib import call
+from cortexmind_amd.data import SplitMix64
+from cortexmind_amd.device import DeviceArray, Stream
+
+pytestmark = pytest.mark.gpu
+
+CAPTURE_RELAXED = 2
+
+
+def hip_rt():
+    h = ctypes.CDLL("libamdhip64.so.7")
+    for name, args in {
+        "hipStreamBeginCapture": [ctypes.c_void_p, ctypes.c_int],
+        "hipStreamEndCapture": [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)],
+        "hipGraphInstantiate": [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_void_p,
+                                ctypes.c_char_p, ctypes.c_size_t],
+        "hipGraphLaunch": [ctypes.c_void_p, ctypes.c_void_p],
+        "hipGraphExecDestroy": [ctypes.c_void_p],
+        "hipGraphDestroy": [ctypes.c_void_p],
+    }.items():
+        getattr(h, name).argtypes = args
+        getattr(h, name).restype = ctypes.c_int
+    return h
+
+
+def capture(h, stream, fn):
+    assert h.hipStreamBeginCapture(stream.handle, CAPTURE_RELAXED) == 0
+    fn()
+    graph = ctypes.c_void_p()
+    assert h.hipStreamEndCapture(stream.handle, ctypes.byref(graph)) == 0
+    exe = ctypes.c_void_p()
+    assert h.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+    return graph, exe
+
+
+@pytest.mark.parametrize("entry,sizes", [
+    ("cxm_reduce_sum_flat_f32", (1 << 24,)),
+    ("cxm_reduce_mean_flat_f32", (1000003,)),
+    ("cxm_reduce_max_flat_f32", (1 << 22,)),
+    ("cxm_reduce_sum_noalloc_f32", (1, 1 << 24, 1)),
+    ("cxm_reduce_sum_noalloc_f32", (3, 500000, 1)),
+])
+def test_replays_match_eager(hip, entry, sizes):
+    h = hip_rt()
+    s = Stream()
+    n = int(np.prod(sizes))
+    n_out = 1 if len(sizes) == 1 else sizes[0] * sizes[2]
+    dx = DeviceArray((n,), np.float32)
+    dz = DeviceArray((n_out,), np.float32)
+    other_x = DeviceArray((1 << 20,), np.float32)
+    other_z = DeviceArray((16,), np.float32)
+    g = SplitMix64(0x6A + n)
+    other_x.upload(g.uniform((1 << 20,), -1.0, 1.0))
+
+    def run():
+        call(entry, dx.ptr, dz.ptr, *sizes, s.handle)
+
+    dx.upload(g.uniform((n,), -1.0, 1.0))
+    run()  # the regions exist before capture
+    s.sync()
+    graph, exe = capture(h, s, run)
+    try:
+        for rep in range(4):
+            x = g.uniform((n,), -1.0, 1.0)
+            dx.upload(x)
+            run()  # eager reference on this data
+            want = dz.numpy(s).copy()
+            dz.fill_bytes(0xFF, s)
+            assert h.hipGraphLaunch(exe, s.handle) == 0
+            got = dz.numpy(s)
+            assert got.tobytes() == want.tobytes(), (entry, rep)
+            # eager reductions of other shapes on the same stream between replays
+            call("cxm_reduce_sum_flat_f32", other_x.ptr, other_z.ptr, (1 << 20) - 5 * rep, s.handle)
+            call("cxm_reduce_sum_noalloc_f32", other_x.ptr, other_z.ptr, 1, (1 << 19) + rep, 1, s.handle)
+            call("cxm_reduce_max_f32", other_x.ptr, other_z.ptr, 16, 1 << 16, 1, s.handle)
+            s.sync()
+    finally:
+        h.hipGraphExecDestroy(exe)
+        h.hipGraphDestroy(graph)
+        s.close()
