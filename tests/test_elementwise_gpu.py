@@ -94,8 +94,12 @@ def f64_act(t, act):
 @pytest.mark.parametrize("act", [ACT_SIGMOID, ACT_TANH, ACT_EXP])
 def test_transcendental_ulp(hip, act):
     g = SplitMix64(41 + act)
+    # sigmoid's results reach the denormal range below t = -87.3 and 0 below
+    # about -103.3; 1 + e^-t overflows below -88.7
     x = np.concatenate([g.normal((1 << 20,), 0.0, 4.0), g.uniform((1 << 18,), -87.0, 88.0),
-                        np.array([0.0, -0.0, 1e-30, -1e-30, 20.0, -20.0, 9.0, -9.0], np.float32)])
+                        g.uniform((1 << 16,), -110.0, -80.0),
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 20.0, -20.0, 9.0, -9.0, -88.7, -88.8, -100.0,
+                                  -150.0, np.inf, -np.inf], np.float32)])
     dx, dz = dev(x), empty(x.shape)
     call("cxm_unary_f32", dx.ptr, dz.ptr, x.size, act, None)
     got = dz.numpy()
