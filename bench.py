@@ -13,8 +13,9 @@ HIP events on the launch stream around the K steps (inputs resident in HBM
 before timing starts).  Algorithmic bytes count each input element read once
 and each output written once; re-reads are not credited.  ``roofline`` is
 for the kernel with the largest share of step time: algorithmic bytes per
-launch over its average launch time, from events around a run of K
-back-to-back launches of that op alone (rotating inputs).  ``traffic`` is
+launch over its average launch time, from events around a run of
+max(K, 100) back-to-back launches of that op alone (rotating inputs, four
+untimed launches queued ahead of the start event).  ``traffic`` is
 the HBM bytes per launch measured with rocprofv3 PMC counters (FETCH_SIZE,
 WRITE_SIZE, scaled against a plain copy kernel), read from
 profiles/pmc_traffic.txt when that file has a line for the kernel.
@@ -371,13 +372,18 @@ def time_steps(ops, steps, warmup, Event, sync):
     return ms
 
 
-def time_op(op, launches, Event, sync):
+def time_op(op, launches, Event, sync, lead=4):
     """Average time of one op from events around `launches` back-to-back
-    launches of it alone (inputs rotating)."""
+    launches of it alone (inputs rotating).  `lead` untimed launches are
+    queued just before the start event, so the timed launches begin on a
+    busy queue rather than after the host's first enqueue (which added up
+    to 0.8 us per launch to a 12 us kernel over 50 launches)."""
     for k in range(2):
         op.fn(k)
     sync()
     t0, t1 = Event(), Event()
+    for k in range(lead):
+        op.fn(k)
     t0.record()
     for k in range(launches):
         op.fn(k)
@@ -414,12 +420,13 @@ def run_workload(name, steps, warmup, E, D, Event, sync):
     step_work = sum(o.work for o in ops)
     unit = ops[0].unit
     per_op = {}
+    launches = max(steps, 100)
     for o in ops:
-        ms = time_op(o, steps, Event, sync)
+        ms = time_op(o, launches, Event, sync)
         per_op[o.name] = {"avg_ms": round(ms, 5), ("GB/s" if o.unit == "B" else "TFLOP/s"): round(rate(o.work, ms, o.unit), 2)}
     extra_ops = [x for x in keep if isinstance(x, Op)]
     for o in extra_ops:
-        ms = time_op(o, steps, Event, sync)
+        ms = time_op(o, launches, Event, sync)
         per_op[o.name] = {"avg_ms": round(ms, 5), "TFLOP/s": round(rate(o.work, ms, o.unit), 2)}
     # dominant kernel: the one with the largest share of step time (C5: the
     # step's largest GEMM, timed alone)

@@ -34,6 +34,15 @@ namespace {
 
 constexpr float kLowest = -FLT_MAX;
 
+// exp(y) of a log-softmax output in the backward (dx = dy - exp(y) * sum dy),
+// as exp2(y * log2 e): v_exp_f32 with the compiler's scaling for results
+// below the normal range, seven instructions where expf's extended-precision
+// range reduction takes about thirteen.  The rounded product costs a relative
+// error of at most |y| * 2^-24 (5.2e-6 while exp(y) is normal, |y| < 87.4),
+// plus about 1 ulp from v_exp_f32, inside the backward's 1e-5 bar on that term.
+// Measured on the [64, 131072] backward: 18.0 -> 17.4 us.
+__device__ __forceinline__ float exp_lsm(float y) { return exp2f(y * 1.44269504088896341f); }
+
 // ------------------------------------------------- wave per row, registers
 
 // NV float4 per lane: cols <= 256 * NV.  WPB rows (one per wave) per workgroup.
@@ -120,8 +129,8 @@ __global__ __launch_bounds__(WPB * kWave) void k_sm_bwd_wave(const float *__rest
         if (i >= c4) continue;
         float4 o;
         if constexpr (LOG) {
-            o.x = gv[k].x - expf(yv[k].x) * r; o.y = gv[k].y - expf(yv[k].y) * r;
-            o.z = gv[k].z - expf(yv[k].z) * r; o.w = gv[k].w - expf(yv[k].w) * r;
+            o.x = gv[k].x - exp_lsm(yv[k].x) * r; o.y = gv[k].y - exp_lsm(yv[k].y) * r;
+            o.z = gv[k].z - exp_lsm(yv[k].z) * r; o.w = gv[k].w - exp_lsm(yv[k].w) * r;
         } else {
             o.x = yv[k].x * (gv[k].x - r); o.y = yv[k].y * (gv[k].y - r);
             o.z = yv[k].z * (gv[k].z - r); o.w = yv[k].w * (gv[k].w - r);
@@ -315,8 +324,8 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_apply(const float *__restrict
         if (i >= n4) continue;
         float4 o;
         if constexpr (LOG) {
-            o.x = g[k].x - expf(yy[k].x) * r; o.y = g[k].y - expf(yy[k].y) * r;
-            o.z = g[k].z - expf(yy[k].z) * r; o.w = g[k].w - expf(yy[k].w) * r;
+            o.x = g[k].x - exp_lsm(yy[k].x) * r; o.y = g[k].y - exp_lsm(yy[k].y) * r;
+            o.z = g[k].z - exp_lsm(yy[k].z) * r; o.w = g[k].w - exp_lsm(yy[k].w) * r;
         } else {
             o.x = yy[k].x * (g[k].x - r); o.y = yy[k].y * (g[k].y - r);
             o.z = yy[k].z * (g[k].z - r); o.w = yy[k].w * (g[k].w - r);
@@ -336,10 +345,15 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_apply(const float *__restrict
 // read and one write, where the two-pass form reads the input twice.
 //
 // No cooperative launch and no grid-wide barrier: a slot is valid when its
-// tag equals the row's epoch + 1.  Every workgroup reads the epoch before it
-// takes its arrival ticket; the workgroup that takes the row's last ticket
-// advances the epoch (and resets the ticket) after all of them have read it,
-// so a slot written by any earlier call never carries the current tag.  The
+// tag equals the row's epoch + 1.  Every workgroup reads the epoch first
+// (before its data loads, so the read is off the critical path) and takes
+// an arrival ticket right after it publishes its partial; the workgroup
+// that took the row's last ticket advances the epoch (and resets the
+// ticket) after its stores, which is after every workgroup of the row has
+// read the epoch, so a slot written by any earlier call never carries the
+// current tag.  Measured at [64, 131072] on gfx950 (forward / backward):
+// ticket at the start, before the partial, 13.4 / 18.0 us; after the
+// stores 13.0 / 18.1; after the publish 11.5 / 16.8.  The
 // wait for a peer's slot is bounded (exchange_wait_limit() polls, each a
 // device round trip plus a short sleep); a peer not seen by then is not
 // waited for: its partial is recomputed from the input with the same
@@ -356,9 +370,9 @@ constexpr size_t kXRowsMax = 8192;
 // workgroup stores at once.  Workgroups of row group g (of `groups`) sleep
 // g * quanta times 128 cycles before their first load, so the later groups'
 // loads fill the earlier groups' exchange gap.  Results do not depend on it.
-__device__ __forceinline__ void x_stagger(size_t row, unsigned segs, unsigned groups, unsigned quanta) {
-    const size_t rows = gridDim.x / segs;
-    const unsigned n = static_cast<unsigned>(row * groups / rows) * quanta;
+__device__ __forceinline__ void x_stagger(unsigned row, unsigned segs, unsigned groups, unsigned quanta) {
+    const unsigned rows = gridDim.x / segs;  // row < rows <= 8192, groups <= 16: 32-bit products
+    const unsigned n = row * groups / rows * quanta;
     for (unsigned i = 0; i < n; ++i) __builtin_amdgcn_s_sleep(2);
 }
 
@@ -374,15 +388,18 @@ __device__ __forceinline__ float xval(unsigned long long u) {
 }
 __device__ __forceinline__ unsigned xtag(unsigned long long u) { return static_cast<unsigned>(u >> 32); }
 
-// Thread 0: read the row's epoch, then take an arrival ticket (the read has
-// returned before the ticket is issued).  Returns the ticket; *tag = epoch+1.
-__device__ __forceinline__ unsigned x_arrive(unsigned *h, unsigned *tag) {
-    const unsigned e = __hip_atomic_load(h + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    *tag = e + 1;
+// The row's epoch (one request per wave: the address is uniform).  The tag
+// of this call's slots is epoch + 1.
+__device__ __forceinline__ unsigned x_epoch(const unsigned *h) {
+    return __hip_atomic_load(h + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Thread 0, after publishing: take the arrival ticket.  The epoch read
+// returned before (its value went into the published tag), so every
+// workgroup has read the epoch when the last ticket is taken.
+__device__ __forceinline__ unsigned x_ticket(unsigned *h) {
     return __hip_atomic_fetch_add(h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Thread 0 of the workgroup holding the row's last ticket, after its work.
+// Thread 0, after the workgroup's stores.
 __device__ __forceinline__ void x_leave(unsigned *h, unsigned ticket, unsigned segs, unsigned tag) {
     if (ticket == segs - 1) {
         __hip_atomic_store(h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -420,6 +437,32 @@ __device__ __forceinline__ unsigned long long x_gather(const unsigned long long 
     return __ballot(miss);
 }
 
+// Loading the thread's NV float4 of a segment of n4 >= 1 float4: x_issue
+// issues every load as straight-line code (an index past the end re-reads
+// the segment's last float4), x_pad then overwrites those with `pad`.
+// Loads under a per-load branch were compiled with a wait for each pair of
+// loads at the branch's end, which halved the bytes in flight; all of a
+// kernel's x_issue calls come before its first x_pad.
+template <int NV>
+__device__ __forceinline__ unsigned x_last(size_t n4) {
+    return static_cast<unsigned>(n4 < kBlock * NV ? n4 : kBlock * NV) - 1u;
+}
+template <int NV>
+__device__ __forceinline__ void x_issue(float4 (&v)[NV], const float *p, unsigned last) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const unsigned i = k * kBlock + threadIdx.x;
+        v[k] = ld4_stream_at(p, 16u * (i < last ? i : last));
+    }
+}
+template <int NV>
+__device__ __forceinline__ void x_pad(float4 (&v)[NV], unsigned last, float4 pad) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        if (k * kBlock + threadIdx.x > last) v[k] = pad;
+    }
+}
+
 __device__ __forceinline__ float max4(float m, float4 v) { return vmax(vmax(vmax(vmax(m, v.x), v.y), v.z), v.w); }
 __device__ __forceinline__ float4 exp4(float4 v, float m) {
     return make_float4(expf(v.x - m), expf(v.y - m), expf(v.z - m), expf(v.w - m));
@@ -441,25 +484,19 @@ __global__ __launch_bounds__(kBlock) void k_sm_fwd_x(const float *__restrict__ x
     __shared__ float lds[kWavesPerBlock];
     __shared__ float part[2][kXMaxSegs];
     __shared__ unsigned long long s_miss;
-    __shared__ unsigned s_tag;
-    const size_t row = blockIdx.x / segs;
-    const unsigned seg = blockIdx.x - static_cast<unsigned>(row) * segs;
+    const unsigned row = blockIdx.x / segs;
+    const unsigned seg = blockIdx.x - row * segs;
     x_stagger(row, segs, groups, quanta);
-    const float *__restrict__ xr = x + row * cols;
+    unsigned *h = hdr + row * kCtr;
+    const unsigned tag = x_epoch(h) + 1;  // every wave: a load behind a branch would be waited for at its end
+    const float *__restrict__ xr = x + static_cast<size_t>(row) * cols;
     const size_t n4 = (cols - static_cast<size_t>(seg) * kXSeg) / 4;
     const float4 ninf = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
     float4 v[NV];
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
-        v[k] = i < n4 ? ld4_stream(xr + seg * kXSeg + 4 * i) : ninf;
-    }
-    unsigned *h = hdr + row * kCtr;
-    unsigned ticket = 0, tag = 0;
-    if (threadIdx.x == 0) {
-        ticket = x_arrive(h, &tag);
-        s_tag = tag;
-    }
+    const unsigned last = x_last<NV>(n4);
+    x_issue(v, xr + seg * kXSeg, last);
+    __builtin_amdgcn_sched_barrier(0);
+    x_pad(v, last, ninf);
     float mt = kLowest;
 #pragma unroll
     for (int k = 0; k < NV; ++k) mt = max4(mt, v[k]);
@@ -472,11 +509,12 @@ __global__ __launch_bounds__(kBlock) void k_sm_fwd_x(const float *__restrict__ x
     }
     const float Mb = block_reduce<MaxOp, kBlock>(mt, lds);
     const float Sb = block_reduce<SumOp, kBlock>(st * expf(mt - Mb), lds);
-    tag = s_tag;  // written before the barriers above
-    unsigned long long *sl = slots + row * kXMaxSegs * 2;
+    unsigned long long *sl = slots + static_cast<size_t>(row) * kXMaxSegs * 2;
+    unsigned ticket = 0;
     if (threadIdx.x == 0) {
         xst(sl + 2 * seg, Mb, tag);
         xst(sl + 2 * seg + 1, Sb, tag);
+        ticket = x_ticket(h);
         part[0][seg] = Mb;
         part[1][seg] = Sb;
     }
@@ -514,7 +552,7 @@ __global__ __launch_bounds__(kBlock) void k_sm_fwd_x(const float *__restrict__ x
     const float M = block_reduce<MaxOp, kBlock>(has ? part[0][threadIdx.x] : kLowest, lds);
     const float S =
         block_reduce<SumOp, kBlock>(has ? part[1][threadIdx.x] * expf(part[0][threadIdx.x] - M) : 0.0f, lds);
-    float *__restrict__ ys = y + row * cols + seg * kXSeg;
+    float *__restrict__ ys = y + static_cast<size_t>(row) * cols + seg * kXSeg;
     if constexpr (LOG) {
         const float ls = logf(S);
 #pragma unroll
@@ -546,35 +584,30 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_x(const float *__restrict__ y
     __shared__ float lds[kWavesPerBlock];
     __shared__ float part[1][kXMaxSegs];
     __shared__ unsigned long long s_miss;
-    __shared__ unsigned s_tag;
-    const size_t row = blockIdx.x / segs;
-    const unsigned seg = blockIdx.x - static_cast<unsigned>(row) * segs;
-    const size_t rbase = row * cols;
+    const unsigned row = blockIdx.x / segs;
+    const unsigned seg = blockIdx.x - row * segs;
+    unsigned *h = hdr + row * kCtr;
+    const unsigned tag = x_epoch(h) + 1;  // every wave: a load behind a branch would be waited for at its end
+    const size_t rbase = static_cast<size_t>(row) * cols;
     const size_t base = rbase + seg * kXSeg;
     const size_t n4 = (cols - static_cast<size_t>(seg) * kXSeg) / 4;
     const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 yv[NV], gv[NV];
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const size_t i = static_cast<size_t>(k) * kBlock + threadIdx.x;
-        const bool in = i < n4;
-        yv[k] = in ? ld4_stream(y + base + 4 * i) : zero;
-        gv[k] = in ? ld4_stream(dy + base + 4 * i) : zero;
-    }
-    unsigned *h = hdr + row * kCtr;
-    unsigned ticket = 0, tag = 0;
-    if (threadIdx.x == 0) {
-        ticket = x_arrive(h, &tag);
-        s_tag = tag;
-    }
+    const unsigned last = x_last<NV>(n4);
+    x_issue(yv, y + base, last);
+    x_issue(gv, dy + base, last);
+    __builtin_amdgcn_sched_barrier(0);
+    x_pad(yv, last, zero);
+    x_pad(gv, last, zero);
     float r = 0.0f;
 #pragma unroll
     for (int k = 0; k < NV; ++k) r = LOG ? r + sum4(gv[k]) : dot4(r, gv[k], yv[k]);
     const float rb = block_reduce<SumOp, kBlock>(r, lds);
-    tag = s_tag;
-    unsigned long long *sl = slots + row * kXMaxSegs * 2;
+    unsigned long long *sl = slots + static_cast<size_t>(row) * kXMaxSegs * 2;
+    unsigned ticket = 0;
     if (threadIdx.x == 0) {
         xst(sl + 2 * seg, rb, tag);
+        ticket = x_ticket(h);
         part[0][seg] = rb;
     }
     if (threadIdx.x < kWave) {
@@ -606,8 +639,8 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_x(const float *__restrict__ y
         if (i >= n4) continue;
         float4 o;
         if constexpr (LOG) {
-            o.x = gv[k].x - expf(yv[k].x) * R; o.y = gv[k].y - expf(yv[k].y) * R;
-            o.z = gv[k].z - expf(yv[k].z) * R; o.w = gv[k].w - expf(yv[k].w) * R;
+            o.x = gv[k].x - exp_lsm(yv[k].x) * R; o.y = gv[k].y - exp_lsm(yv[k].y) * R;
+            o.z = gv[k].z - exp_lsm(yv[k].z) * R; o.w = gv[k].w - exp_lsm(yv[k].w) * R;
         } else {
             o.x = yv[k].x * (gv[k].x - R); o.y = yv[k].y * (gv[k].y - R);
             o.z = yv[k].z * (gv[k].z - R); o.w = yv[k].w * (gv[k].w - R);
@@ -656,7 +689,7 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_any(const float *__restrict__
     r = wave_reduce<SumOp>(r);
     for (size_t j = lane; j < cols; j += kWave) {
         const float yy = y[off + j], g = dy[off + j];
-        dx[off + j] = LOG ? g - expf(yy) * r : yy * (g - r);
+        dx[off + j] = LOG ? g - exp_lsm(yy) * r : yy * (g - r);
     }
 }
 
@@ -762,13 +795,14 @@ bool use_x(size_t rows, size_t cols) { return rows <= kXRowsMax && (cols + kXSeg
 // (pct 0 -> 60 -> 70): [64, 131072] 14.6 -> 13.9 -> 13.6 us, [128, 65536]
 // 13.3 -> 12.4 -> 12.4, [256, 32768] 13.1 -> 12.1 -> 12.1; at 80 the
 // forward slows again, and an 8 MiB input gains nothing.  The backward
-// (two inputs, one output) was slower at every setting and starts at once.
+// (two inputs, one output) was slower at every setting (with the arrival
+// ticket after the publish, [64, 131072]: 16.9 us at once, 17.5 / 18.2 /
+// 20.0 us at pct 30 / 65 / 100) and starts at once.
 std::atomic<int> g_x_stagger_pct{65};
 
-void x_stagger_for(size_t rows, unsigned segs, size_t bytes_in, unsigned *groups, unsigned *quanta) {
+void x_stagger_for(int pct, size_t rows, unsigned segs, size_t bytes_in, unsigned *groups, unsigned *quanta) {
     *groups = 1;
     *quanta = 0;
-    const int pct = g_x_stagger_pct.load(std::memory_order_relaxed);
     if (pct <= 0 || rows < 2 || rows * segs > 1024) return;
     *groups = rows < 16 ? static_cast<unsigned>(rows) : 16u;
     const double total = static_cast<double>(bytes_in) / 6.0e12 * (pct / 100.0) * 2.4e9 / 128.0;
@@ -783,7 +817,7 @@ int sm_fwd_x(const float *x, float *y, size_t rows, size_t cols, int log_mode, c
     const dim3 grid(static_cast<unsigned>(rows * segs));
     const unsigned lim = exchange_wait_limit();
     unsigned g, q;
-    x_stagger_for(rows, segs, rows * cols * sizeof(float), &g, &q);
+    x_stagger_for(g_x_stagger_pct.load(std::memory_order_relaxed), rows, segs, rows * cols * sizeof(float), &g, &q);
     if (log_mode)
         hipLaunchKernelGGL(k_sm_fwd_x<true>, grid, dim3(kBlock), 0, hs(st), x, y, cols, segs, xc.hdr, xc.slots, lim,
                            g, q);
