@@ -714,8 +714,9 @@ __global__ __launch_bounds__(kW4Threads) void k_gemm_w4(const float *__restrict_
 // operand), filled by direct global-to-LDS loads (lds_load16) four steps
 // ahead, so three tiles are in flight while one is multiplied.  The
 // stage of step t is refilled with tile t+4 right after the ring barrier
-// that follows its last fragment read.  For M, N multiples of 128 and a K
-// range per split that is a multiple of 128.
+// that follows its last fragment read.  For a K range per split that is a
+// multiple of 128; a partial last tile along M or N (the non-k-contiguous
+// operand's row length a multiple of 4) loads clamped rows.
 // Stage layouts (16-byte chunks XOR-keyed so that fragment reads are
 // conflict-free across the 64 banks):
 //  * k-contiguous operand (A [M,K], B^T [N,K]): row r of 32 floats, chunk c
@@ -736,17 +737,24 @@ __device__ __forceinline__ int rk_m(int k) { return 8 * ((k >> 2) & 1); }
 // Fills one operand stage: k-contiguous X[r][k] (ld = K) at rows r0..,
 // k0..: eight rows of 32 floats per instruction; else X[k][r] (ld = row
 // length) at k rows k0.., columns r0..: two k rows of 128 floats each.
+// `rlast` clamps the global row (KC) or 4-column group start (otherwise) of
+// a partial last tile to the operand's last one: rows or columns past the
+// operand's end load duplicates, whose products land only in accumulator
+// rows or columns that the epilogue does not store.
 template <bool KC>
-__device__ __forceinline__ void ring_fill(const float *__restrict__ X, size_t r0, size_t k0, size_t ld, float *stage) {
+__device__ __forceinline__ void ring_fill(const float *__restrict__ X, size_t r0, size_t k0, size_t ld, size_t rlast,
+                                          float *stage) {
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         if constexpr (KC) {
             const int rb = w * 32 + s * 8, row = rb + (lane >> 3), p = lane & 7;
-            lds_load16(X + (r0 + row) * ld + k0 + 4 * (p ^ rk_c(row)), stage + rb * kRBK);
+            const size_t gr = r0 + row < rlast ? r0 + row : rlast;
+            lds_load16(X + gr * ld + k0 + 4 * (p ^ rk_c(row)), stage + rb * kRBK);
         } else {
             const int kb = w * 8 + s * 2, kr = kb + (lane >> 5), p = lane & 31;
-            lds_load16(X + (k0 + kr) * ld + r0 + 4 * (p ^ rk_m(kr)), stage + kb * BM);
+            const size_t gc = r0 + 4 * (p ^ rk_m(kr));
+            lds_load16(X + (k0 + kr) * ld + (gc < rlast ? gc : rlast), stage + kb * BM);
         }
     }
 }
@@ -801,8 +809,9 @@ __device__ __forceinline__ void ring_block(const RingFrag &f, floatx16 (&acc)[2]
 // holds block 0 of cur on entry and block 0 of nxt on return.
 template <bool KCA, bool KCB>
 __device__ __forceinline__ void ring_step(const float *__restrict__ A, const float *__restrict__ B, size_t lda,
-                                          size_t ldb, size_t m0, size_t n0, size_t kf, float *cur, const float *nxt,
-                                          RingFrag &f0, floatx16 (&acc)[2][2], int wm, int wn, int l32, int lhi) {
+                                          size_t ldb, size_t m0, size_t n0, size_t ra, size_t rb, size_t kf,
+                                          float *cur, const float *nxt, RingFrag &f0, floatx16 (&acc)[2][2], int wm,
+                                          int wn, int l32, int lhi) {
     RingFrag f1, f2;
     ring_frags<KCA, KCB>(cur, 1, wm, wn, l32, lhi, f1);
     ring_block<KCA, KCB>(f0, acc);
@@ -812,8 +821,8 @@ __device__ __forceinline__ void ring_step(const float *__restrict__ A, const flo
     ring_block<KCA, KCB>(f2, acc);
     ring_barrier<2 * kRPS>();  // tile t+1 landed; every wave done reading cur
     ring_frags<KCA, KCB>(nxt, 0, wm, wn, l32, lhi, f0);
-    ring_fill<KCA>(A, m0, kf, lda, cur);
-    ring_fill<KCB>(B, n0, kf, ldb, cur + kRST);
+    ring_fill<KCA>(A, m0, kf, lda, ra, cur);
+    ring_fill<KCB>(B, n0, kf, ldb, rb, cur + kRST);
     ring_block<KCA, KCB>(f1, acc);
 }
 
@@ -837,6 +846,7 @@ __global__ __launch_bounds__(kRingThreads) void k_gemm_ring(const float *__restr
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int wm = wave >> 1, wn = wave & 1, l32 = lane & 31, lhi = lane >> 5;
     const size_t lda = KCA ? K : M, ldb = KCB ? K : N;
+    const size_t ra = KCA ? M - 1 : M - 4, rb = KCB ? N - 1 : N - 4;  // ring_fill's clamps
 
     floatx16 acc[2][2];
 #pragma unroll
@@ -850,22 +860,22 @@ __global__ __launch_bounds__(kRingThreads) void k_gemm_ring(const float *__restr
     // beyond T-1 reload tile T-1 into stages whose fragments go unused.
     const size_t T = (kend - kbeg) / kRBK;
     auto kt = [&](size_t t) { return kbeg + (t < T ? t : T - 1) * kRBK; };
-    ring_fill<KCA>(A, m0, kt(0), lda, s0);
-    ring_fill<KCB>(B, n0, kt(0), ldb, s0 + kRST);
-    ring_fill<KCA>(A, m0, kt(1), lda, s1);
-    ring_fill<KCB>(B, n0, kt(1), ldb, s1 + kRST);
-    ring_fill<KCA>(A, m0, kt(2), lda, s2);
-    ring_fill<KCB>(B, n0, kt(2), ldb, s2 + kRST);
-    ring_fill<KCA>(A, m0, kt(3), lda, s3);
-    ring_fill<KCB>(B, n0, kt(3), ldb, s3 + kRST);
+    ring_fill<KCA>(A, m0, kt(0), lda, ra, s0);
+    ring_fill<KCB>(B, n0, kt(0), ldb, rb, s0 + kRST);
+    ring_fill<KCA>(A, m0, kt(1), lda, ra, s1);
+    ring_fill<KCB>(B, n0, kt(1), ldb, rb, s1 + kRST);
+    ring_fill<KCA>(A, m0, kt(2), lda, ra, s2);
+    ring_fill<KCB>(B, n0, kt(2), ldb, rb, s2 + kRST);
+    ring_fill<KCA>(A, m0, kt(3), lda, ra, s3);
+    ring_fill<KCB>(B, n0, kt(3), ldb, rb, s3 + kRST);
     ring_barrier<3 * kRPS>();
     RingFrag f0;
     ring_frags<KCA, KCB>(s0, 0, wm, wn, l32, lhi, f0);
     for (size_t t = 0; t < T; t += 4) {
-        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, kt(t + 4), s0, s1, f0, acc, wm, wn, l32, lhi);
-        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, kt(t + 5), s1, s2, f0, acc, wm, wn, l32, lhi);
-        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, kt(t + 6), s2, s3, f0, acc, wm, wn, l32, lhi);
-        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, kt(t + 7), s3, s0, f0, acc, wm, wn, l32, lhi);
+        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, ra, rb, kt(t + 4), s0, s1, f0, acc, wm, wn, l32, lhi);
+        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, ra, rb, kt(t + 5), s1, s2, f0, acc, wm, wn, l32, lhi);
+        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, ra, rb, kt(t + 6), s2, s3, f0, acc, wm, wn, l32, lhi);
+        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, ra, rb, kt(t + 7), s3, s0, f0, acc, wm, wn, l32, lhi);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
     gemm_epilogue<2, 2>(acc, C, M, N, m0, n0, tile, split, splits, wm, wn, lhi, l32, epi, part, counters, &flag);
@@ -1235,7 +1245,10 @@ int gemm_ex(const float *A, const float *B, float *C, size_t M, size_t K, size_t
     }
     // a split's k range is a whole number of the kernel's k steps (the
     // ring's: four stages of 32)
-    const bool ring_ok = M % BM == 0 && N % BN == 0 && K % (4 * kRBK) == 0 && aligned16(A) && aligned16(B);
+    // the ring: whole 128-k steps; a partial last M or N tile is clamped,
+    // which needs the [K, M] / [K, N] storage's row length a multiple of 4
+    const bool ring_ok = K % (4 * kRBK) == 0 && aligned16(A) && aligned16(B) && M >= 4 && N >= 4 &&
+                         (!ta || M % 4 == 0) && (tb || N % 4 == 0);
     const int variant = gemm_variant(ta, tb, static_cast<unsigned>(tiles * splits), ring_ok);
     const size_t kstep = variant == 7 ? 4 * kRBK : (variant == 2 || variant == 4) ? 64 : BK;
     size_t kper = (K + splits - 1) / splits;

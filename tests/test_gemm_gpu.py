@@ -107,11 +107,14 @@ def test_ring_same_bits_as_kc(hip, m, k, n, tb):
     assert np.all(np.abs(r7 - a.astype(np.float64) @ b.astype(np.float64)) <= bound(a, b))
 
 
-@pytest.mark.parametrize("m,k,n", [(256, 4096, 256), (384, 512, 640)], ids=lambda v: str(v))
+@pytest.mark.parametrize("m,k,n", [(256, 4096, 256), (384, 512, 640), (300, 512, 260), (36, 256, 516),
+                                   (784, 4096, 1024)], ids=lambda v: str(v))
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
 def test_ring_all_forms_float64(hip, m, k, n, ta, tb):
     """Variant 7 pinned for every stored form with the bias + ReLU epilogue;
-    256 x 4096 x 256 has 4 tiles and splits K 16 ways (256 each)."""
+    256 x 4096 x 256 has 4 tiles and splits K 16 ways (256 each); 300 x 260,
+    36 x 516 and 784 x 1024 (the MLP's first weight gradient) end in partial
+    tiles, whose rows or columns past the operand load clamped duplicates."""
     g = SplitMix64(31 * m + k + 7 * n + 3 * ta + tb)
     a, b = g.normal((m, k)), g.normal((k, n))
     bias = g.normal((n,), 0.0, 0.5)
