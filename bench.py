@@ -627,7 +627,7 @@ def main():
     if not args.no_extra:
         wl = {}
         for name in [w for w in ["c1", "c3", "c4", "c5", "more", "g16"] if w != args.workload]:
-            r = run_workload(name, max(5, args.steps // 5), 2, E, D, Event, sync)
+            r = run_workload(name, max(20, args.steps // 2), 2, E, D, Event, sync)
             wl[name] = {"workload": r["config"]["workload"], "value": round(r["value"], 2),
                         "unit": r["unit"], "ms_per_step": round(r["ms_per_step"], 5),
                         "roofline": r["roofline"], "per_op": r["per_op"]}
