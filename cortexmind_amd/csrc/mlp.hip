@@ -22,13 +22,13 @@
 //
 // The output layer (d3 <= 16 classes, d2 <= 1024, d2 % 4 == 0) runs as one
 // "head" kernel per 16 rows of the batch: logits = h2 W3 + b3, the softmax
-// cross-entropy, dl, and dh2 = (dl W3^T) * [h2 > 0] from one read of h2, with
-// per-workgroup partial sums of the loss, of dl's columns (gb3) and of
-// dh2's columns (gb2); a small finish kernel adds the partials in
-// workgroup order and applies loss / B and the two bias SGD steps.  The
-// unfused chain (thin GEMM, cross-entropy, thin GEMM, two column sums) ran
-// 50 us at the C5 shape, most of it launch and latency; the arithmetic of
-// each logit, dl and dh2 element is the unfused kernels' own.
+// cross-entropy, its gradient dl, and dh2 = (dl W3^T) * [h2 > 0] from one read of h2, with
+// per-workgroup partial sums of the loss, of dl's columns (gb3), of dh2's
+// columns (gb2) and of h2^T dl (gW3); a finish kernel adds the partials in
+// workgroup order and applies loss / B and the b3, b2 and W3 SGD steps.  The
+// unfused chain (thin GEMMs for the logits, dh2 and gW3, the cross-entropy,
+// two column sums) ran 67 us at the C5 shape, most of it launch and latency;
+// the fused pair runs 21 us.
 #include <cfloat>
 #include <new>
 
@@ -37,7 +37,7 @@
 struct cxm_mlp3 {
     size_t b, d0, d1, d2, d3;
     float *h1, *h2, *lg, *dl, *dh2, *dh1;
-    float *part;  // head partials [blocks][d2 + 16] (fused head only)
+    float *part;  // head partials [blocks][head_part_width(d2, d3)] (fused head only)
     unsigned head_blocks;
     int fused_head;  // 1: the fused output layer (d3 <= 16, d2 <= 1024, d2 % 4 == 0); 0: unfused
     void *block;  // one allocation holding all of the above
@@ -50,6 +50,8 @@ constexpr int kHeadThreads = 1024;
 constexpr int kHeadRows = 16;  // rows per workgroup: the 16 of a 16x16 MFMA tile
 constexpr int kHeadMaxD2 = 1024;
 constexpr int kHeadExtra = 16;  // partial columns after the d2 of gb2: loss, then gb3[0..d3-1]
+// A head workgroup's partial row: gb2 [D2], the loss and gb3 [16], gW3 [D3][D2].
+__host__ __device__ inline size_t head_part_width(size_t d2, size_t d3) { return d2 + kHeadExtra + d3 * d2; }
 
 // One workgroup of 16 waves: rows r0 .. r0 + 15 of the batch; wave w owns
 // columns k in [64 w, 64 w + 64) of h2 (and rows of W3).  Both products run
@@ -74,8 +76,8 @@ constexpr int kHeadExtra = 16;  // partial columns after the d2 of gb2: loss, th
 // in LDS to Wk[k][c] (row stride 20 floats, zero past D3 and D2), for
 // which the B reads of step 1 (lanes (c, q): rows 4 q + e, column c) and
 // the A reads of step 3 (lanes (kk, q): row kk, columns 4 q ..) meet no
-// bank conflicts.  Writes dl [B, D3], dh2 [B, D2] and part[blockIdx] =
-// (colsum dh2 [D2], nll sum, colsum dl [D3]).
+// bank conflicts.  Writes dh2 [B, D2] and part[blockIdx] =
+// (colsum dh2 [D2], nll sum, colsum dl [D3], gW3 [D3][D2]).
 constexpr int kWkStride = 20;
 constexpr int kHeadW3PerThread = kHeadMaxD2 * 16 / kHeadThreads;
 
@@ -98,7 +100,7 @@ __global__ __launch_bounds__(kHeadThreads) void k_mlp_head(const float *__restri
                                                            const float *__restrict__ w3,
                                                            const float *__restrict__ b3,
                                                            const int32_t *__restrict__ labels,
-                                                           float *__restrict__ dl, float *__restrict__ dh2,
+                                                           float *__restrict__ dh2,
                                                            size_t B, size_t D2, size_t D3, float inv_b,
                                                            float *__restrict__ part) {
     constexpr int NW = kHeadThreads / kWave;
@@ -178,7 +180,6 @@ __global__ __launch_bounds__(kHeadThreads) void k_mlp_head(const float *__restri
         float p = e / s;
         if (l16 == lab) p = p - 1.0f;
         const float d = (cin && valid) ? p * inv_b : 0.0f;
-        if (cin && valid) dl[(r0 + row) * D3 + l16] = d;
         dt[row][l16] = d;
         const bool ok = lab >= 0 && lab < nc;
         const float nll = row16_sum(l16 == lab ? -((v - m) - logf(s)) : 0.0f);
@@ -226,7 +227,32 @@ __global__ __launch_bounds__(kHeadThreads) void k_mlp_head(const float *__restri
     for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[blk][i] += dpp<kRowMirror>(o[blk][i]);
-    float *__restrict__ prow = part + static_cast<size_t>(blockIdx.x) * (D2 + kHeadExtra);
+    float *__restrict__ prow = part + static_cast<size_t>(blockIdx.x) * head_part_width(D2, D3);
+
+    // 4. gW3 over the 16 rows, G[k][c] = sum_b h2[b][k] dl[b][c], on the same MFMA with the
+    //    contraction over b: MFMA j takes A[kk][q] = h2[4 j + q][k + kk] (lane (kk, q)) and
+    //    B[q][c] = dl[4 j + q][c].  Lane (kk, q) fetches its A value from the lane that holds
+    //    it, (4 j + q) + 16 (kk / 4), component kk % 4 of a[blk] (ds_bpermute, all four
+    //    components, then a select); lane (c, q) receives G[k + 4 q + i][c], stored as a float4
+    //    into the workgroup's [D3][D2] partial.
+    float *__restrict__ pg = prow + D2 + kHeadExtra;
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+        f32x4 g = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int src = ((4 * j + q) + 16 * (l16 >> 2)) * 4;
+            const float v0 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, a[blk].x)));
+            const float v1 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, a[blk].y)));
+            const float v2 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, a[blk].z)));
+            const float v3 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, a[blk].w)));
+            const int e = l16 & 3;
+            const float av = e == 0 ? v0 : e == 1 ? v1 : e == 2 ? v2 : v3;
+            g = __builtin_amdgcn_mfma_f32_16x16x4f32(av, dt[4 * j + q][l16], g, 0, 0, 0);
+        }
+        const size_t kk = 64 * w + 16 * blk + 4 * q;
+        if (l16 < nc && kk < D2) *reinterpret_cast<float4 *>(pg + l16 * D2 + kk) = make_float4(g[0], g[1], g[2], g[3]);
+    }
     if (l16 == 0) {
 #pragma unroll
         for (int blk = 0; blk < 4; ++blk) {
@@ -247,18 +273,19 @@ __global__ __launch_bounds__(kHeadThreads) void k_mlp_head(const float *__restri
 
 // Column c of the partials: the sum over workgroups p = q, q + 16, ... per
 // thread (q = threadIdx.x / 64), then the 16 thread sums in q order.
-// Columns < D2: b2 -= lr * sum; D2: *loss = sum / B; D2 + 1 + n: b3[n] -= lr * sum.
+// Columns < D2: b2 -= lr * sum; D2: *loss = sum / B; D2 + 1 + n: b3[n] -= lr * sum;
+// D2 + 16 + c D2 + k: W3[k][c] -= lr * sum.
 constexpr int kFinishThreads = 1024;
 constexpr int kFinishCols = 64;
 __global__ __launch_bounds__(kFinishThreads) void k_head_finish(const float *__restrict__ part, unsigned blocks,
                                                                 size_t D2, size_t D3, size_t B, float lr,
                                                                 float *__restrict__ loss, float *__restrict__ b2,
-                                                                float *__restrict__ b3) {
+                                                                float *__restrict__ b3, float *__restrict__ w3) {
     constexpr int Q = kFinishThreads / kFinishCols;
     __shared__ float acc[Q][kFinishCols];
     const int c = threadIdx.x % kFinishCols, q = threadIdx.x / kFinishCols;
     const size_t col = static_cast<size_t>(blockIdx.x) * kFinishCols + c;
-    const size_t pw = D2 + kHeadExtra;
+    const size_t pw = head_part_width(D2, D3);
     float v = 0.0f;
     if (col < pw) {
         constexpr unsigned G = 16;
@@ -284,23 +311,29 @@ __global__ __launch_bounds__(kFinishThreads) void k_head_finish(const float *__r
         b2[col] = b2[col] - t;
     } else if (col == D2) {
         loss[0] = g / static_cast<float>(B);
-    } else if (col - D2 - 1 < D3) {
+    } else if (col < D2 + kHeadExtra) {
+        if (col - D2 - 1 < D3) {
+            const float t = g * lr;
+            b3[col - D2 - 1] = b3[col - D2 - 1] - t;
+        }
+    } else {
+        const size_t i = col - D2 - kHeadExtra, cls = i / D2, k = i - cls * D2;
         const float t = g * lr;
-        b3[col - D2 - 1] = b3[col - D2 - 1] - t;
+        w3[k * D3 + cls] = w3[k * D3 + cls] - t;
     }
 }
 
 
-int run_head(const cxm_mlp3 *h, const int32_t *labels, const float *w3, float *b3, float *b2, float lr,
-             float *loss, hipStream_t s) {
+int run_head(const cxm_mlp3 *h, const int32_t *labels, float *w3, float *b3, float *b2, float lr, float *loss,
+             hipStream_t s) {
     const float inv_b = 1.0f / static_cast<float>(h->b);
-    hipLaunchKernelGGL(k_mlp_head, dim3(h->head_blocks), dim3(kHeadThreads), 0, s, h->h2, w3, b3, labels, h->dl,
+    hipLaunchKernelGGL(k_mlp_head, dim3(h->head_blocks), dim3(kHeadThreads), 0, s, h->h2, w3, b3, labels,
                        h->dh2, h->b, h->d2, h->d3, inv_b, h->part);
     int rc = launch_status();
     if (rc) return rc;
-    const size_t pw = h->d2 + kHeadExtra;
+    const size_t pw = head_part_width(h->d2, h->d3);
     hipLaunchKernelGGL(k_head_finish, dim3(ceil_div(pw, kFinishCols)), dim3(kFinishThreads), 0, s, h->part,
-                       h->head_blocks, h->d2, h->d3, h->b, lr, loss, b2, b3);
+                       h->head_blocks, h->d2, h->d3, h->b, lr, loss, b2, b3, w3);
     return launch_status();
 }
 
@@ -326,7 +359,7 @@ int cxm_mlp3_create(cxm_mlp3 **handle, size_t batch, size_t d0, size_t d1, size_
     // sizes in floats, each rounded to 64 floats (256 B) to keep 128-bit alignment
     auto r = [](size_t n) { return (n + 63) / 64 * 64; };
     const size_t sizes[7] = {r(batch * d1), r(batch * d2), r(batch * d3), r(batch * d3),
-                             r(batch * d2), r(batch * d1), h->fused_head ? r(blocks * (d2 + cxm::kHeadExtra)) : 0};
+                             r(batch * d2), r(batch * d1), h->fused_head ? r(blocks * cxm::head_part_width(d2, d3)) : 0};
     size_t total = 0;
     for (size_t s : sizes) total += s;
     void *p = nullptr;
@@ -368,9 +401,8 @@ int cxm_mlp3_step_f32(cxm_mlp3 *h, const float *x, const int32_t *labels, float 
     CXM_TRY(cxm::gemm_ex(x, w1, h->h1, B, d0, d1, 0, 0, Epilogue{b1, nullptr, CXM_ACT_RELU, 0, 0.0f}, s));
     CXM_TRY(cxm::gemm_ex(h->h1, w2, h->h2, B, d1, d2, 0, 0, Epilogue{b2, nullptr, CXM_ACT_RELU, 0, 0.0f}, s));
     if (h->fused_head) {
-        // output layer fused: logits, loss, dl, dh2 (reads W3), then b3 and b2
+        // output layer fused: logits, loss, dl, dh2 (reads W3), then the loss, b3, b2 and W3 updates
         CXM_TRY(cxm::run_head(h, labels, w3, b3, b2, lr, loss, reinterpret_cast<hipStream_t>(s)));
-        CXM_TRY(cxm::gemm_ex(h->h2, h->dl, w3, d2, B, d3, 1, 0, sgd, s));
     } else {
         CXM_TRY(cxm::gemm_ex(h->h2, w3, h->lg, B, d2, d3, 0, 0, Epilogue{b3, nullptr, CXM_ACT_NONE, 0, 0.0f}, s));
         CXM_TRY(cxm_softmax_xent_f32(h->lg, labels, loss, h->dl, B, d3, s));
