@@ -714,9 +714,10 @@ __global__ __launch_bounds__(kW4Threads) void k_gemm_w4(const float *__restrict_
 // operand), filled by direct global-to-LDS loads (lds_load16) four steps
 // ahead, so three tiles are in flight while one is multiplied.  The
 // stage of step t is refilled with tile t+4 right after the ring barrier
-// that follows its last fragment read.  For a K range per split that is a
-// multiple of 128; a partial last tile along M or N (the non-k-contiguous
-// operand's row length a multiple of 4) loads clamped rows.
+// that follows its last fragment read.  K a multiple of 8 (a split's range
+// a multiple of 128 but for the last split's; the last 32-k stage runs its
+// whole 8-k blocks only); a partial last tile along M or N (the
+// non-k-contiguous operand's row length a multiple of 4) loads clamped rows.
 // Stage layouts (16-byte chunks XOR-keyed so that fragment reads are
 // conflict-free across the 64 banks):
 //  * k-contiguous operand (A [M,K], B^T [N,K]): row r of 32 floats, chunk c
@@ -740,21 +741,24 @@ __device__ __forceinline__ int rk_m(int k) { return 8 * ((k >> 2) & 1); }
 // `rlast` clamps the global row (KC) or 4-column group start (otherwise) of
 // a partial last tile to the operand's last one: rows or columns past the
 // operand's end load duplicates, whose products land only in accumulator
-// rows or columns that the epilogue does not store.
-template <bool KC>
+// rows or columns that the epilogue does not store.  `klast` clamps k the
+// same way (the last 4-k group start for KC, else the last k row): a
+// stage that runs past K loads duplicates into 8-k blocks that are never
+// multiplied (ring_last).
+template <bool KC, bool TAIL>
 __device__ __forceinline__ void ring_fill(const float *__restrict__ X, size_t r0, size_t k0, size_t ld, size_t rlast,
-                                          float *stage) {
+                                          size_t klast, float *stage) {
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         if constexpr (KC) {
             const int rb = w * 32 + s * 8, row = rb + (lane >> 3), p = lane & 7;
-            const size_t gr = r0 + row < rlast ? r0 + row : rlast;
-            lds_load16(X + gr * ld + k0 + 4 * (p ^ rk_c(row)), stage + rb * kRBK);
+            const size_t gr = r0 + row < rlast ? r0 + row : rlast, gk = k0 + 4 * (p ^ rk_c(row));
+            lds_load16(X + gr * ld + (!TAIL || gk < klast ? gk : klast), stage + rb * kRBK);
         } else {
             const int kb = w * 8 + s * 2, kr = kb + (lane >> 5), p = lane & 31;
-            const size_t gc = r0 + 4 * (p ^ rk_m(kr));
-            lds_load16(X + (k0 + kr) * ld + (gc < rlast ? gc : rlast), stage + kb * BM);
+            const size_t gc = r0 + 4 * (p ^ rk_m(kr)), gk = k0 + kr;
+            lds_load16(X + (!TAIL || gk < klast ? gk : klast) * ld + (gc < rlast ? gc : rlast), stage + kb * BM);
         }
     }
 }
@@ -807,11 +811,11 @@ __device__ __forceinline__ void ring_block(const RingFrag &f, floatx16 (&acc)[2]
 
 // Step on stage cur (tile t; A at +0, B at +kRST); nxt holds tile t+1; f0
 // holds block 0 of cur on entry and block 0 of nxt on return.
-template <bool KCA, bool KCB>
+template <bool KCA, bool KCB, bool TAIL>
 __device__ __forceinline__ void ring_step(const float *__restrict__ A, const float *__restrict__ B, size_t lda,
-                                          size_t ldb, size_t m0, size_t n0, size_t ra, size_t rb, size_t kf,
-                                          float *cur, const float *nxt, RingFrag &f0, floatx16 (&acc)[2][2], int wm,
-                                          int wn, int l32, int lhi) {
+                                          size_t ldb, size_t m0, size_t n0, size_t ra, size_t rb, size_t ka,
+                                          size_t kb, size_t kf, float *cur, const float *nxt, RingFrag &f0,
+                                          floatx16 (&acc)[2][2], int wm, int wn, int l32, int lhi) {
     RingFrag f1, f2;
     ring_frags<KCA, KCB>(cur, 1, wm, wn, l32, lhi, f1);
     ring_block<KCA, KCB>(f0, acc);
@@ -821,14 +825,30 @@ __device__ __forceinline__ void ring_step(const float *__restrict__ A, const flo
     ring_block<KCA, KCB>(f2, acc);
     ring_barrier<2 * kRPS>();  // tile t+1 landed; every wave done reading cur
     ring_frags<KCA, KCB>(nxt, 0, wm, wn, l32, lhi, f0);
-    ring_fill<KCA>(A, m0, kf, lda, ra, cur);
-    ring_fill<KCB>(B, n0, kf, ldb, rb, cur + kRST);
+    ring_fill<KCA, TAIL>(A, m0, kf, lda, ra, ka, cur);
+    ring_fill<KCB, TAIL>(B, n0, kf, ldb, rb, kb, cur + kRST);
     ring_block<KCA, KCB>(f1, acc);
 }
 
-// Same arguments as k_gemm.  KCA: A stored [M,K] (else [K,M]); KCB: B stored
-// [N,K] (else [K,N]).
+// The last k tile, on stage cur (landed; f0 holds its block 0): its first
+// nb 8-k blocks only (1 <= nb <= 4), no refill.
 template <bool KCA, bool KCB>
+__device__ __forceinline__ void ring_last(const float *cur, const RingFrag &f0, int nb, floatx16 (&acc)[2][2], int wm,
+                                          int wn, int l32, int lhi) {
+    ring_block<KCA, KCB>(f0, acc);
+    for (int kb = 1; kb < nb; ++kb) {  // nb is uniform
+        RingFrag f;
+        ring_frags<KCA, KCB>(cur, kb, wm, wn, l32, lhi, f);
+        ring_block<KCA, KCB>(f, acc);
+    }
+}
+
+// Same arguments as k_gemm.  KCA: A stored [M,K] (else [K,M]); KCB: B stored
+// [N,K] (else [K,N]).  TAIL: a split's k range may end in a partial 32-k
+// stage (K not a multiple of 128).  A separate instance: the tail's extra
+// steps and clamps, compiled into the one loop, moved the accumulators'
+// neighbours into AGPRs and slowed every whole-stage product by 2-3 us.
+template <bool KCA, bool KCB, bool TAIL>
 __global__ __launch_bounds__(kRingThreads) void k_gemm_ring(const float *__restrict__ A, const float *__restrict__ B,
                                                             float *__restrict__ C, size_t M, size_t N, size_t K,
                                                             unsigned tiles_n, unsigned splits, size_t kper,
@@ -847,6 +867,7 @@ __global__ __launch_bounds__(kRingThreads) void k_gemm_ring(const float *__restr
     const int wm = wave >> 1, wn = wave & 1, l32 = lane & 31, lhi = lane >> 5;
     const size_t lda = KCA ? K : M, ldb = KCB ? K : N;
     const size_t ra = KCA ? M - 1 : M - 4, rb = KCB ? N - 1 : N - 4;  // ring_fill's clamps
+    const size_t ka = KCA ? K - 4 : K - 1, kb = KCB ? K - 4 : K - 1;
 
     floatx16 acc[2][2];
 #pragma unroll
@@ -856,27 +877,60 @@ __global__ __launch_bounds__(kRingThreads) void k_gemm_ring(const float *__restr
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // (kend - kbeg) % 128 == 0: tiles 0..T-1, T a multiple of 4.  Tiles
-    // beyond T-1 reload tile T-1 into stages whose fragments go unused.
-    const size_t T = (kend - kbeg) / kRBK;
+    // (kend - kbeg) % 8 == 0 (% 128 == 0 without TAIL): tiles 0..T-1 of 32
+    // k, the last with nb 8-k blocks.  Tiles beyond T-1 reload tile T-1
+    // into stages whose fragments go unused.
+    const size_t len = kend - kbeg, T = (len + kRBK - 1) / kRBK;
     auto kt = [&](size_t t) { return kbeg + (t < T ? t : T - 1) * kRBK; };
-    ring_fill<KCA>(A, m0, kt(0), lda, ra, s0);
-    ring_fill<KCB>(B, n0, kt(0), ldb, rb, s0 + kRST);
-    ring_fill<KCA>(A, m0, kt(1), lda, ra, s1);
-    ring_fill<KCB>(B, n0, kt(1), ldb, rb, s1 + kRST);
-    ring_fill<KCA>(A, m0, kt(2), lda, ra, s2);
-    ring_fill<KCB>(B, n0, kt(2), ldb, rb, s2 + kRST);
-    ring_fill<KCA>(A, m0, kt(3), lda, ra, s3);
-    ring_fill<KCB>(B, n0, kt(3), ldb, rb, s3 + kRST);
+    ring_fill<KCA, TAIL>(A, m0, kt(0), lda, ra, ka, s0);
+    ring_fill<KCB, TAIL>(B, n0, kt(0), ldb, rb, kb, s0 + kRST);
+    ring_fill<KCA, TAIL>(A, m0, kt(1), lda, ra, ka, s1);
+    ring_fill<KCB, TAIL>(B, n0, kt(1), ldb, rb, kb, s1 + kRST);
+    ring_fill<KCA, TAIL>(A, m0, kt(2), lda, ra, ka, s2);
+    ring_fill<KCB, TAIL>(B, n0, kt(2), ldb, rb, kb, s2 + kRST);
+    ring_fill<KCA, TAIL>(A, m0, kt(3), lda, ra, ka, s3);
+    ring_fill<KCB, TAIL>(B, n0, kt(3), ldb, rb, kb, s3 + kRST);
     ring_barrier<3 * kRPS>();
     RingFrag f0;
     ring_frags<KCA, KCB>(s0, 0, wm, wn, l32, lhi, f0);
-    for (size_t t = 0; t < T; t += 4) {
-        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, ra, rb, kt(t + 4), s0, s1, f0, acc, wm, wn, l32, lhi);
-        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, ra, rb, kt(t + 5), s1, s2, f0, acc, wm, wn, l32, lhi);
-        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, ra, rb, kt(t + 6), s2, s3, f0, acc, wm, wn, l32, lhi);
-        ring_step<KCA, KCB>(A, B, lda, ldb, m0, n0, ra, rb, kt(t + 7), s3, s0, f0, acc, wm, wn, l32, lhi);
+#define CXM_RING_STEP(T4, CUR, NXT) \
+    ring_step<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kt(T4), CUR, NXT, f0, acc, wm, wn, l32, lhi)
+    if constexpr (!TAIL) {
+        for (size_t t = 0; t < T; t += 4) {  // T is a multiple of 4
+            CXM_RING_STEP(t + 4, s0, s1);
+            CXM_RING_STEP(t + 5, s1, s2);
+            CXM_RING_STEP(t + 6, s2, s3);
+            CXM_RING_STEP(t + 7, s3, s0);
+        }
+    } else {
+        const int nb = static_cast<int>((len - (T - 1) * kRBK) / 8);
+        size_t t = 0;
+        for (; t + 4 < T; t += 4) {
+            CXM_RING_STEP(t + 4, s0, s1);
+            CXM_RING_STEP(t + 5, s1, s2);
+            CXM_RING_STEP(t + 6, s2, s3);
+            CXM_RING_STEP(t + 7, s3, s0);
+        }
+        // tiles t .. T-1 remain (one to four), tile t on s0
+        const size_t rem = T - t;
+        if (rem == 1) {
+            ring_last<KCA, KCB>(s0, f0, nb, acc, wm, wn, l32, lhi);
+        } else {
+            CXM_RING_STEP(t + 4, s0, s1);
+            if (rem == 2) {
+                ring_last<KCA, KCB>(s1, f0, nb, acc, wm, wn, l32, lhi);
+            } else {
+                CXM_RING_STEP(t + 5, s1, s2);
+                if (rem == 3) {
+                    ring_last<KCA, KCB>(s2, f0, nb, acc, wm, wn, l32, lhi);
+                } else {
+                    CXM_RING_STEP(t + 6, s2, s3);
+                    ring_last<KCA, KCB>(s3, f0, nb, acc, wm, wn, l32, lhi);
+                }
+            }
+        }
     }
+#undef CXM_RING_STEP
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
     gemm_epilogue<2, 2>(acc, C, M, N, m0, n0, tile, split, splits, wm, wn, lhi, l32, epi, part, counters, &flag);
 }
@@ -1140,8 +1194,12 @@ int launch_t(const float *A, const float *B, float *C, size_t M, size_t N, size_
              dim3 grid, unsigned tiles_n, unsigned splits, size_t kper, Epilogue epi, float *part,
              unsigned *counters, hipStream_t s, int variant) {
     if (variant == 7) {
-        hipLaunchKernelGGL((k_gemm_ring<!TA, TB>), grid, dim3(kRingThreads), 0, s, A, B, C, M, N, K, tiles_n, splits,
-                           kper, epi, part, counters);
+        if (K % (4 * kRBK) == 0)
+            hipLaunchKernelGGL((k_gemm_ring<!TA, TB, false>), grid, dim3(kRingThreads), 0, s, A, B, C, M, N, K, tiles_n,
+                               splits, kper, epi, part, counters);
+        else
+            hipLaunchKernelGGL((k_gemm_ring<!TA, TB, true>), grid, dim3(kRingThreads), 0, s, A, B, C, M, N, K, tiles_n,
+                               splits, kper, epi, part, counters);
         return launch_status();
     }
 #define CXM_GEMM_LAUNCH(VA_, VB_)                                                                  \
@@ -1245,9 +1303,9 @@ int gemm_ex(const float *A, const float *B, float *C, size_t M, size_t K, size_t
     }
     // a split's k range is a whole number of the kernel's k steps (the
     // ring's: four stages of 32)
-    // the ring: whole 128-k steps; a partial last M or N tile is clamped,
+    // the ring: whole 8-k blocks; a partial last M or N tile is clamped,
     // which needs the [K, M] / [K, N] storage's row length a multiple of 4
-    const bool ring_ok = K % (4 * kRBK) == 0 && aligned16(A) && aligned16(B) && M >= 4 && N >= 4 &&
+    const bool ring_ok = K % 8 == 0 && aligned16(A) && aligned16(B) && M >= 4 && N >= 4 &&
                          (!ta || M % 4 == 0) && (tb || N % 4 == 0);
     const int variant = gemm_variant(ta, tb, static_cast<unsigned>(tiles * splits), ring_ok);
     const size_t kstep = variant == 7 ? 4 * kRBK : (variant == 2 || variant == 4) ? 64 : BK;

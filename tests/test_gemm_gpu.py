@@ -88,12 +88,17 @@ def _pin(variant):
     assert lib().cxm_gemm_f32_kernel(variant) == 0
 
 
-@pytest.mark.parametrize("m,k,n", [(128, 128, 128), (256, 384, 512), (512, 1024, 256)], ids=lambda v: str(v))
+@pytest.mark.parametrize("m,k,n", [(128, 128, 128), (256, 384, 512), (512, 1024, 256), (2048, 784, 1536),
+                                   (128, 40, 256)], ids=lambda v: str(v))
 @pytest.mark.parametrize("tb", [0, 1])
 def test_ring_same_bits_as_kc(hip, m, k, n, tb):
     """The direct-to-LDS ring (variant 7) and the k-contiguous kernel
     (variant 1) sum each output over k in the same order, so A B and A B^T
-    agree bitwise; both within the bound of the float64 product."""
+    agree bitwise; both within the bound of the float64 product.  Shapes
+    whose K both kernels split alike (none, or 1024 four ways): the ring
+    rounds a split's range to 128 k, the other kernel to 32.  K = 784 and 40
+    end in a partial stage, of which the ring multiplies only the whole 8-k
+    blocks and the other kernel zero-fills the rest."""
     g = SplitMix64(m + 5 * k + 9 * n + tb)
     a, b = g.normal((m, k)), g.normal((k, n))
     try:
@@ -108,13 +113,16 @@ def test_ring_same_bits_as_kc(hip, m, k, n, tb):
 
 
 @pytest.mark.parametrize("m,k,n", [(256, 4096, 256), (384, 512, 640), (300, 512, 260), (36, 256, 516),
-                                   (784, 4096, 1024)], ids=lambda v: str(v))
+                                   (784, 4096, 1024), (300, 784, 260), (128, 8, 128), (256, 4104, 256)],
+                         ids=lambda v: str(v))
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
 def test_ring_all_forms_float64(hip, m, k, n, ta, tb):
     """Variant 7 pinned for every stored form with the bias + ReLU epilogue;
     256 x 4096 x 256 has 4 tiles and splits K 16 ways (256 each); 300 x 260,
     36 x 516 and 784 x 1024 (the MLP's first weight gradient) end in partial
-    tiles, whose rows or columns past the operand load clamped duplicates."""
+    tiles, whose rows or columns past the operand load clamped duplicates;
+    K = 784, 8 and 4104 (a split whose last range is 8 k) end in a partial
+    32-k stage, of which only the whole 8-k blocks are multiplied."""
     g = SplitMix64(31 * m + k + 7 * n + 3 * ta + tb)
     a, b = g.normal((m, k)), g.normal((k, n))
     bias = g.normal((n,), 0.0, 0.5)
