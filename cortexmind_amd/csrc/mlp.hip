@@ -49,8 +49,10 @@ namespace {
 constexpr int kHeadThreads = 1024;
 constexpr int kHeadRows = 16;  // rows per workgroup: the 16 of a 16x16 MFMA tile
 constexpr int kHeadMaxD2 = 1024;
-constexpr int kHeadExtra = 16;  // partial columns after the d2 of gb2: loss, then gb3[0..d3-1]
-// A head workgroup's partial row: gb2 [D2], the loss and gb3 [16], gW3 [D3][D2].
+// partial columns after the d2 of gb2: the loss, then gb3[0..d3-1] (up to
+// 17 values; 32 keeps the gW3 columns that follow 16-byte aligned)
+constexpr int kHeadExtra = 32;
+// A head workgroup's partial row: gb2 [D2], the loss and gb3 [kHeadExtra], gW3 [D3][D2].
 __host__ __device__ inline size_t head_part_width(size_t d2, size_t d3) { return d2 + kHeadExtra + d3 * d2; }
 
 // One workgroup of 16 waves: rows r0 .. r0 + 15 of the batch; wave w owns

@@ -8,7 +8,8 @@ with g++ against the in-tree library:
     small integers), including matmul's shape inference;
   * tests/cpp/graph_test (include/cortex_hip_graph.hpp) checks Storage /
     Tensor::to / the caching pool, that three SGD steps of the MLP through
-    the GradientFlow graph are bit-identical to cxm_mlp3_step_f32, and
+    the GradientFlow graph agree with cxm_mlp3_step_f32 (losses within 1e-5
+    relative, parameters within 1e-4 of their weight scale), and
     gradient accumulation over two consumers."""
 import os
 import subprocess

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from cortexmind_amd import engine
-from cortexmind_amd.data import c5_mlp
+from cortexmind_amd.data import SplitMix64, c5_mlp
 
 from gpu_util import dev, empty
 
@@ -89,3 +89,25 @@ def test_mlp_full_size_ten_steps_vs_oracle(hip, orc):
         print(f"{k}: max |gpu - oracle| {errs[k][0]:.3e} (bar {errs[k][1]:.3e})", flush=True)
     assert all(e <= bar for e, bar in errs.values()), errs
     assert all(np.isfinite(losses)) and losses[-1] < losses[0]
+
+
+@pytest.mark.parametrize("batch,dims", [(100, (49, 64, 36, 3)), (37, (20, 40, 1024, 16)), (300, (784, 128, 96, 10)),
+                                        (64, (16, 24, 1028, 10)), (16, (8, 8, 4, 1))], ids=lambda v: str(v))
+def test_mlp_shapes_vs_oracle(hip, orc, batch, dims):
+    """The fused output layer (d3 <= 16, d2 <= 1024, d2 % 4 == 0) at batch
+    sizes off its 16-row tile, with 1, 3 and 16 classes and d2 from 4 to its
+    1024 limit; d2 = 1028 takes the unfused kernels.  Random biases, three
+    steps at lr 0.05 against the oracle's step, same bars as above."""
+    x, labels, params = c5_mlp(batch=batch, dims=dims)
+    g = SplitMix64(77 + batch)
+    for k in ("b1", "b2", "b3"):
+        params[k] = g.normal(params[k].shape, 0.0, 0.1)
+    losses, final = gpu_steps(x, labels, params, 0.05, 3)
+    ref = {k: v.copy() for k, v in params.items()}
+    ref_losses = [orc.mlp_step(x, labels, ref, 0.05) for _ in range(3)]
+    for got, want in zip(losses, ref_losses):
+        assert abs(got - want) <= 1e-5 * max(abs(want), 1e-3), (losses, ref_losses)
+    for k in ref:
+        w = "w" + k[1]
+        scale = max(np.abs(params[w]).max(), np.abs(ref[w]).max())
+        assert np.max(np.abs(final[k] - ref[k])) <= 1e-4 * scale, k
