@@ -220,7 +220,7 @@ __device__ __forceinline__ RowSplit split_row(const float *xr, size_t dim) {
 // tail elements.  Writers and a reader that recomputes a segment both call
 // it, so a recomputed partial has the writer's bits.  Element indices (the
 // arg operators) count from the row start; kShift operators get x - xr[0].
-template <class Op, int UNR>
+template <class Op, int UNR, bool ONE = false>
 __device__ __forceinline__ typename Op::T row_segment(const float *__restrict__ xr, size_t dim, unsigned seg,
                                                       size_t seg4, typename Op::T *lds) {
     using T = typename Op::T;
@@ -239,6 +239,22 @@ __device__ __forceinline__ typename Op::T row_segment(const float *__restrict__ 
     const float *__restrict__ sb = xr + sp.h + 4 * b4;
     const int off = static_cast<int>(sp.h + 4 * b4);
     unsigned j = tid;
+    if (ONE && __builtin_expect(n4 == UNR * kBlock, 1)) {
+        // ONE (the flat writers): one whole batch, every segment but the
+        // last in the flat plan, as straight-line code, the loads leaving
+        // before any fold.  Without the scheduling barrier the compiler
+        // folded the first float4 before issuing the other seven, a memory
+        // round trip per workgroup; with it the flat sum went 12.8 -> 12.3
+        // us (with the reader's one-barrier check below).  The row plans
+        // keep the loop: the row argmax lost 0.2 us to this form
+        float4 v[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) v[u] = ld4_stream_at(sb, 16u * (j + u * kBlock));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], off + static_cast<int>(4 * (j + u * kBlock)), 1, k4);
+        j = n4;
+    }
     for (; j + (UNR - 1) * kBlock < n4; j += UNR * kBlock) {
         float4 v[UNR];
 #pragma unroll
@@ -327,25 +343,54 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
                     }
                 }
             }
+            // The block's combine carries whether any slot was missed: with
+            // none (the rule) the result is out after one barrier.  A
+            // __syncthreads_or ahead of the combine cost three barriers on
+            // the kernel's critical path (0.2-0.3 us).
+            T a = Op::identity();
+#pragma unroll
+            for (int k = 0; k < IT; ++k)
+                if (tid + k * kBlock < segs) a = Op::combine(a, val[k]);
+            {
+                __shared__ unsigned wmiss[kWavesPerBlock];
+                a = wave_reduce<Op>(a);
+                const unsigned wm = __ballot(miss != 0u) != 0ull ? 1u : 0u;
+                if ((tid & (kWave - 1)) == 0) {
+                    lds[tid / kWave] = a;
+                    wmiss[tid / kWave] = wm;
+                }
+                __syncthreads();
+                unsigned any = 0;
+#pragma unroll
+                for (int w = 0; w < kWavesPerBlock; ++w) any |= wmiss[w];
+                if (any == 0u) {  // block_reduce's order: waves 0, 1, 2, 3
+                    if (tid == 0) {
+                        T r = lds[0];
+#pragma unroll
+                        for (int w = 1; w < kWavesPerBlock; ++w) r = Op::combine(r, lds[w]);
+                        write_out<Op>(out, 0, r);
+                    }
+                    return;
+                }
+                __syncthreads();  // lds is reused below
+            }
             // segments not seen in time (none, unless the wait limit is
             // small): recomputed by the whole workgroup with one load in
             // flight per thread -- the writer's fold order (each thread folds
             // its float4s in index order whatever the unroll), so its bits
-            if (__syncthreads_or(miss != 0u)) {
-                lmiss[tid] = miss;
-                __syncthreads();
-                for (unsigned i = 0; i < segs; ++i) {
-                    const unsigned t = i % kBlock, k = i / kBlock;
-                    if (!((lmiss[t] >> k) & 1u)) continue;  // uniform: every thread reads the same word
-                    const T r = row_segment<Op, 1>(x, dim, i, seg4, lds);
-                    if (tid == static_cast<int>(t)) {
+            lmiss[tid] = miss;
+            __syncthreads();
+            for (unsigned i = 0; i < segs; ++i) {
+                const unsigned t = i % kBlock, k = i / kBlock;
+                if (!((lmiss[t] >> k) & 1u)) continue;  // uniform: every thread reads the same word
+                const T r = row_segment<Op, 1>(x, dim, i, seg4, lds);
+                if (tid == static_cast<int>(t)) {
 #pragma unroll
-                        for (int q = 0; q < IT; ++q)
-                            if (q == static_cast<int>(k)) val[q] = r;
-                    }
+                    for (int q = 0; q < IT; ++q)
+                        if (q == static_cast<int>(k)) val[q] = r;
                 }
             }
-            T a = Op::identity();
+            a = Op::identity();
 #pragma unroll
             for (int k = 0; k < IT; ++k)
                 if (tid + k * kBlock < segs) a = Op::combine(a, val[k]);
@@ -354,7 +399,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
             return;
         }
         // a writer
-        const T r = row_segment<Op, UNR>(x, dim, blockIdx.x, seg4, lds);
+        const T r = row_segment<Op, UNR, true>(x, dim, blockIdx.x, seg4, lds);
         if (tid == 0) {
             const unsigned long long v = (static_cast<unsigned long long>(epoch) << 32) | __builtin_bit_cast(unsigned, r);
             __hip_atomic_store(slots + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -423,13 +468,24 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
     __shared__ T lds[NSLOT][kColTile];
     __shared__ int flag;
 
-    // 32-bit divisions: the grid has fewer than 2^31 workgroups (a 64-bit
-    // division is a long software sequence ahead of every thread's first load)
-    const unsigned b = blockIdx.x;
-    const unsigned q = b / chunks;
-    const unsigned chunk = b - q * chunks;
-    const unsigned tile = q % ntiles;
-    const size_t o = q / ntiles;
+    // FAST launches a (chunks, tiles, outer) grid: no index arithmetic ahead
+    // of the first load (the two divisions of a flat grid's index took some
+    // 60 instructions; decoding either form behind a branch made the
+    // compiler load the kernel arguments in two rounds).  Other forms take a
+    // flat grid, decoded with 32-bit divisions (fewer than 2^31 workgroups).
+    unsigned chunk, tile;
+    size_t o;
+    if constexpr (FAST) {
+        chunk = blockIdx.x;
+        tile = blockIdx.y;
+        o = blockIdx.z;
+    } else {
+        const unsigned b = blockIdx.x;
+        const unsigned q = b / chunks;
+        chunk = b - q * chunks;
+        tile = q % ntiles;
+        o = q / ntiles;
+    }
     const int tid = threadIdx.x;
     const float *__restrict__ xo = x + o * dim * inner;
     const size_t r0 = chunk * rows_per_chunk;
@@ -455,11 +511,17 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
                 const float *__restrict__ cb = xo + r0 * inner + static_cast<size_t>(tile) * kColTile;
                 const unsigned rowb = static_cast<unsigned>(inner * sizeof(float)), nr = static_cast<unsigned>(r1 - r0);
                 const unsigned c16 = static_cast<unsigned>(lane * 16);
-                unsigned r = w;
-                for (; r + (UNR - 1) * NW < nr; r += UNR * NW) {
+                // row offsets as a per-lane column offset plus uniform row
+                // offsets (the wave index made uniform, so the products are
+                // scalar): a multiply per load had put 16 quarter-rate vector
+                // multiplies between the index arithmetic and the first load
+                const unsigned wu = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(w));
+                const unsigned step = NW * rowb;
+                unsigned r = wu, ro = wu * rowb + c16;
+                for (; r + (UNR - 1) * NW < nr; r += UNR * NW, ro += UNR * step) {
                     float4 v[UNR];
 #pragma unroll
-                    for (int u = 0; u < UNR; ++u) v[u] = ld4_stream_at(cb, (r + u * NW) * rowb + c16);
+                    for (int u = 0; u < UNR; ++u) v[u] = ld4_stream_at(cb, ro + u * step);
                     // all UNR loads leave before any is folded: left alone, the
                     // scheduler interleaved the folds to stay at 64 registers
                     // and kept 5-6 loads in flight (one 16-wave workgroup per
@@ -468,7 +530,7 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
 #pragma unroll
                     for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], static_cast<int>(r0 + r + u * NW), 0, k4);
                 }
-                for (; r < nr; r += NW) fold4<Op>(acc, ld4_stream_at(cb, r * rowb + c16), static_cast<int>(r0 + r), 0, k4);
+                for (; r < nr; r += NW, ro += step) fold4<Op>(acc, ld4_stream_at(cb, ro), static_cast<int>(r0 + r), 0, k4);
             } else {
                 size_t r = r0 + w;
                 for (; r + (UNR - 1) * NW < r1; r += UNR * NW) {
@@ -632,17 +694,23 @@ int run_cols_plan(const float *x, size_t outer, size_t dim, size_t inner, OutDes
         part = static_cast<T *>(sc.part);
         counters = sc.counters;
     }
-    const unsigned nb = static_cast<unsigned>(blocks);
     const unsigned nt = static_cast<unsigned>(ntiles), nc = static_cast<unsigned>(chunks);
-    // whole tiles and 32-bit byte offsets within a chunk (under 2^31 bytes)
-    const bool fast = inner % kColTile == 0 && (rpc * inner + kColTile) * sizeof(float) < (size_t(1) << 31);
+    // FAST: whole float4 tiles and 32-bit byte offsets within a chunk (under
+    // 2^31 bytes), on a (chunks, tiles, outer) grid, so tiles and outer
+    // slices must fit its y and z dimensions; other forms take a flat grid,
+    // whose work-item count is a 32-bit field of the dispatch
+    const bool fast = vec && inner % kColTile == 0 &&
+                      (rpc * inner + kColTile) * sizeof(float) < (size_t(1) << 31) && ntiles <= 65535 &&
+                      outer <= 65535;
+    if (!fast && blocks * static_cast<size_t>(plan.nw) * kWave > 0xffffffffu) return CXM_E_TOO_LARGE;
+    const dim3 grid = fast ? dim3(nc, nt, static_cast<unsigned>(outer)) : dim3(static_cast<unsigned>(blocks));
 #define CXM_COLS(VEC_, UNR_, NW_)                                                                              \
     do {                                                                                                       \
         if (VEC_ && fast)                                                                                      \
-            hipLaunchKernelGGL((k_cols<Op, VEC_, UNR_, NW_, true>), dim3(nb), dim3(NW_ * kWave), 0, hs, x, dim, \
+            hipLaunchKernelGGL((k_cols<Op, VEC_, UNR_, NW_, true>), grid, dim3(NW_ * kWave), 0, hs, x, dim,      \
                                inner, nt, nc, rpc, part, counters, out);                                       \
         else                                                                                                   \
-            hipLaunchKernelGGL((k_cols<Op, VEC_, UNR_, NW_>), dim3(nb), dim3(NW_ * kWave), 0, hs, x, dim, inner, \
+            hipLaunchKernelGGL((k_cols<Op, VEC_, UNR_, NW_>), grid, dim3(NW_ * kWave), 0, hs, x, dim, inner,      \
                                nt, nc, rpc, part, counters, out);                                              \
     } while (0)
     if (plan.nw == 16) {

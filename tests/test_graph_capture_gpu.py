@@ -54,6 +54,8 @@ def capture(h, stream, fn):
     ("cxm_reduce_max_flat_f32", (1 << 22,)),
     ("cxm_reduce_sum_noalloc_f32", (1, 1 << 24, 1)),
     ("cxm_reduce_sum_noalloc_f32", (3, 500000, 1)),
+    ("cxm_reduce_sum_f32", (1, 4096, 4096)),
+    ("cxm_reduce_max_f32", (2, 3000, 512)),
 ])
 def test_replays_match_eager(hip, entry, sizes):
     h = hip_rt()
@@ -63,7 +65,7 @@ def test_replays_match_eager(hip, entry, sizes):
     dx = DeviceArray((n,), np.float32)
     dz = DeviceArray((n_out,), np.float32)
     other_x = DeviceArray((1 << 20,), np.float32)
-    other_z = DeviceArray((16,), np.float32)
+    other_z = DeviceArray((256,), np.float32)
     g = SplitMix64(0x6A + n)
     other_x.upload(g.uniform((1 << 20,), -1.0, 1.0))
 
@@ -88,6 +90,7 @@ def test_replays_match_eager(hip, entry, sizes):
             call("cxm_reduce_sum_flat_f32", other_x.ptr, other_z.ptr, (1 << 20) - 5 * rep, s.handle)
             call("cxm_reduce_sum_noalloc_f32", other_x.ptr, other_z.ptr, 1, (1 << 19) + rep, 1, s.handle)
             call("cxm_reduce_max_f32", other_x.ptr, other_z.ptr, 16, 1 << 16, 1, s.handle)
+            call("cxm_reduce_sum_f32", other_x.ptr, other_z.ptr, 1, 4096 - 16 * rep, 256, s.handle)
             s.sync()
     finally:
         h.hipGraphExecDestroy(exe)
