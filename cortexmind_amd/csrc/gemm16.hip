@@ -776,14 +776,20 @@ __global__ __launch_bounds__(kHThreads) void k_gemm16_ring(const uint16_t *__res
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
 
+    // the tile origin again, from the workgroup index: kept live across the
+    // K loop it was spilled to scratch (all 512 registers hold the
+    // accumulators and the ring's fragments there)
+    group_tile(xcd_remap16(blockIdx.x, gridDim.x), static_cast<unsigned>(M / TM), tiles_n, gm, &tm, &tn);
+    const size_t em0 = static_cast<size_t>(__builtin_amdgcn_readfirstlane(tm)) * TM;
+    const size_t en0 = static_cast<size_t>(__builtin_amdgcn_readfirstlane(tn)) * TM;
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            const size_t col = n0 + wn * (TM / 2) + j * 32 + l32;
+            const size_t col = en0 + wn * (TM / 2) + j * 32 + l32;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const size_t row = m0 + wm * (TM / 2) + i * 32 + 8 * (r / 4) + 4 * lhi + (r % 4);
+                const size_t row = em0 + wm * (TM / 2) + i * 32 + 8 * (r / 4) + 4 * lhi + (r % 4);
                 C[row * N + col] = H<DT>::store(acc[i][j][r]);
             }
         }
