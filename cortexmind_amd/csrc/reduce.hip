@@ -293,6 +293,18 @@ __device__ __forceinline__ typename Op::T row_segment(const float *__restrict__ 
 // gfx950 for a 64 MiB flat sum, two-level ticket 13.1 us, one reader
 // polling tagged slots 12.0-12.3 us, streaming alone 11.2 us.  Both combine
 // the same partials in the same order, so their results are bit-identical.
+// MODE 3 is MODE 2 under a tag that recurs (a graph replays the captured
+// one; the static region's callers may be captured): the reader empties
+// each slot it used and marks each one it gave up on, and a writer that
+// finds the mark empties its slot, so that no partial outlives the kernel
+// (`clear` is the host's record of that choice: 1 exactly in MODE 3).
+// MODE 2 leaves slots as they are: no later call carries their tag.
+//
+// The mark is the tag ~epoch, which no partial of the call carries.
+__device__ __forceinline__ unsigned long long miss_mark(unsigned epoch) {
+    return static_cast<unsigned long long>(~epoch) << 32;
+}
+
 template <class Op, int UNR, int MODE>
 __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, size_t dim, unsigned segs, size_t seg4,
                                                  typename Op::T *__restrict__ part, unsigned *__restrict__ counters,
@@ -303,8 +315,11 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
     __shared__ int flag;
     const int tid = threadIdx.x;
 
-    if constexpr (MODE == 2) {
+    if constexpr (MODE >= 2) {
         static_assert(sizeof(T) == 4, "tagged slots carry 32-bit partials");
+        // MODE 3: the tag is one a graph replays (or the static region's),
+        // so slots are emptied after use and given-up ones marked
+        constexpr bool CLEAR = MODE == 3;
         constexpr int IT = kMaxFlatSegs / kBlock;
         if (blockIdx.x == segs) {  // the reader
             // The first loads are unconditional (the slot regions hold at
@@ -337,7 +352,24 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
                     }
                     if (static_cast<unsigned>(w >> 32) == epoch) {
                         val[k] = __builtin_bit_cast(T, static_cast<unsigned>(w));
-                        if (clear) __hip_atomic_store(slots + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        // `clear` is 0 in MODE 2; tested at run time there all
+                        // the same: with the store compiled out, the compiler
+                        // kept every copy of val[] live (70 registers, not 46)
+                        if (CLEAR || clear) __hip_atomic_store(slots + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    } else if constexpr (CLEAR) {
+                        // Given up under a tag that a graph replays: leave a
+                        // mark, so that the late writer empties the slot
+                        // rather than leave its partial, tagged, for the next
+                        // replay to take as its own.  A partial that landed
+                        // in between is taken after all.
+                        const unsigned long long o = __hip_atomic_exchange(slots + i, miss_mark(epoch), __ATOMIC_RELAXED,
+                                                                           __HIP_MEMORY_SCOPE_AGENT);
+                        if (static_cast<unsigned>(o >> 32) == epoch) {
+                            val[k] = __builtin_bit_cast(T, static_cast<unsigned>(o));
+                            __hip_atomic_store(slots + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        } else {
+                            miss |= 1u << k;
+                        }
                     } else {
                         miss |= 1u << k;
                     }
@@ -402,7 +434,16 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
         const T r = row_segment<Op, UNR, true>(x, dim, blockIdx.x, seg4, lds);
         if (tid == 0) {
             const unsigned long long v = (static_cast<unsigned long long>(epoch) << 32) | __builtin_bit_cast(unsigned, r);
-            __hip_atomic_store(slots + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if constexpr (CLEAR) {
+                // the reader's mark: it recomputed this partial, and the slot
+                // goes back to empty (under a replayed tag nothing else would
+                // clear it)
+                if (__hip_atomic_exchange(slots + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    miss_mark(epoch))
+                    __hip_atomic_store(slots + blockIdx.x, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                __hip_atomic_store(slots + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
         return;
     } else {
@@ -643,10 +684,14 @@ int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t 
         tg = sc.tagged;
     }
     const unsigned grid = mode == 2 ? nb + 1 : nb;
+    const bool replayed = mode == 2 && tg.clear;  // MODE 3
 #define CXM_ROWS(U, M) launch_rows<Op, U, M>(grid, hs, x, dim, sg, seg4, part, counters, tg, out)
     if (mode == 0) { if (unr8) CXM_ROWS(8, 0); else CXM_ROWS(4, 0); }
     else if (mode == 1) { if (unr8) CXM_ROWS(8, 1); else CXM_ROWS(4, 1); }
-    else if constexpr (sizeof(T) == 4) { if (unr8) CXM_ROWS(8, 2); else CXM_ROWS(4, 2); }
+    else if constexpr (sizeof(T) == 4) {
+        if (replayed) { if (unr8) CXM_ROWS(8, 3); else CXM_ROWS(4, 3); }
+        else { if (unr8) CXM_ROWS(8, 2); else CXM_ROWS(4, 2); }
+    }
 #undef CXM_ROWS
     return launch_status();
 }

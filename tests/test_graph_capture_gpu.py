@@ -96,3 +96,59 @@ def test_replays_match_eager(hip, entry, sizes):
         h.hipGraphExecDestroy(exe)
         h.hipGraphDestroy(graph)
         s.close()
+
+
+def _wait_limit(polls):
+    old = ctypes.c_uint(0)
+    call("cxm_exchange_wait_limit", polls, ctypes.byref(old))
+    return old.value
+
+
+@pytest.mark.parametrize("entry,sizes", [
+    ("cxm_reduce_sum_flat_f32", (1 << 24,)),
+    ("cxm_reduce_sum_noalloc_f32", (1, 1 << 24, 1)),
+])
+def test_replays_after_missed_slots(hip, entry, sizes):
+    """Captured with a wait limit of 0, the reader gives up on every slot
+    not yet written when it looks and recomputes that partial; the late
+    writer's slot must not survive into the next replay, which reuses the
+    captured tag (it would be taken for that replay's partial).  Every
+    replay, on new data, gives the bits of an eager call."""
+    h = hip_rt()
+    s = Stream()
+    n = int(np.prod(sizes))
+    dx = DeviceArray((n,), np.float32)
+    dz = DeviceArray((1,), np.float32)
+    g = SplitMix64(0x6B + n)
+
+    def run():
+        call(entry, dx.ptr, dz.ptr, *sizes, s.handle)
+
+    dx.upload(g.uniform((n,), -1.0, 1.0))
+    run()
+    s.sync()
+    old = _wait_limit(0)
+    try:
+        graph, exe = capture(h, s, run)
+    finally:
+        _wait_limit(old)
+    try:
+        # eager results first: an eager call between replays would overwrite
+        # every slot with its own tag and hide a stale one
+        xs = [g.uniform((n,), -1.0, 1.0) for _ in range(6)]
+        wants = []
+        for x in xs:
+            dx.upload(x)
+            run()  # default wait limit
+            wants.append(dz.numpy(s).copy())
+        for rep, x in enumerate(xs):
+            dx.upload(x)
+            dz.fill_bytes(0xFF, s)
+            assert h.hipGraphLaunch(exe, s.handle) == 0
+            got = dz.numpy(s)
+            assert got.tobytes() == wants[rep].tobytes(), (entry, rep, got, wants[rep])
+            s.sync()
+    finally:
+        h.hipGraphExecDestroy(exe)
+        h.hipGraphDestroy(graph)
+        s.close()
