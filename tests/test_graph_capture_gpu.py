@@ -1,4 +1,5 @@
-"""Reductions captured into a HIP graph and replayed.
+"""Reductions (and, in the last test, the long-row softmax, a split-K GEMM
+and the MLP step) captured into a HIP graph and replayed.
 
 A flat reduction's writers tag their partials with a per-call tag that a
 graph replays unchanged, so a call made under stream capture has its reader
@@ -151,4 +152,66 @@ def test_replays_after_missed_slots(hip, entry, sizes):
     finally:
         h.hipGraphExecDestroy(exe)
         h.hipGraphDestroy(graph)
+        s.close()
+
+
+def test_capture_softmax_gemm_mlp_step(hip):
+    """The long-row softmax (its row exchange keeps a device-side epoch),
+    a split-K weight-gradient GEMM (ticket counters) and the full C5 MLP step
+    (fused head, split-K SGD epilogues) captured into one graph and replayed
+    on new inputs: every replay gives the eager bits."""
+    from cortexmind_amd.data import c5_mlp
+    from cortexmind_amd import engine
+
+    h = hip_rt()
+    s = Stream()
+    g = SplitMix64(0x6C)
+    R, C = 64, 131072
+    sx, sy, sg, sdx = (DeviceArray((R * C,), np.float32) for _ in range(4))
+    M, K, N = 1024, 4096, 1024
+    ga, gb, gc = DeviceArray((K * M,), np.float32), DeviceArray((K * N,), np.float32), DeviceArray((M * N,), np.float32)
+    x, labels, params0 = c5_mlp()
+    net = engine.Mlp3(x.shape[0], 784, 1024, 1024, 10)
+    dx_m, dlab, dloss = DeviceArray.from_numpy(x), DeviceArray.from_numpy(labels), DeviceArray((1,), np.float32)
+    dp = {k: DeviceArray.from_numpy(v) for k, v in params0.items()}
+
+    def run():
+        call("cxm_softmax_fwd_f32", sx.ptr, sy.ptr, R, C, 0, s.handle)
+        call("cxm_softmax_bwd_f32", sy.ptr, sg.ptr, sdx.ptr, R, C, 0, s.handle)
+        call("cxm_gemm_f32", ga.ptr, gb.ptr, gc.ptr, M, K, N, 1, 0, None, 0, None, s.handle)
+        net.step(dx_m, dlab, dp, 0.01, dloss, s)
+
+    def new_inputs():
+        sx.upload(g.uniform((R * C,), -4.0, 4.0))
+        sg.upload(g.uniform((R * C,), -1.0, 1.0))
+        ga.upload(g.uniform((K * M,), -1.0, 1.0))
+        gb.upload(g.uniform((K * N,), -1.0, 1.0))
+        dx_m.upload(g.uniform(x.shape, -1.0, 1.0))
+        for k, v in params0.items():
+            dp[k].upload(v)
+
+    def outputs():
+        outs = [sy.numpy(s), sdx.numpy(s), gc.numpy(s), dloss.numpy(s)]
+        return outs + [dp[k].numpy(s) for k in sorted(dp)]
+
+    new_inputs()
+    run()  # the workspaces exist before capture
+    s.sync()
+    graph, exe = capture(h, s, run)
+    try:
+        for rep in range(3):
+            new_inputs()
+            assert h.hipGraphLaunch(exe, s.handle) == 0
+            got = outputs()
+            for k, v in params0.items():  # same start for the eager step
+                dp[k].upload(v)
+            run()
+            want = outputs()
+            for i, (a, b) in enumerate(zip(got, want)):
+                assert a.tobytes() == b.tobytes(), (rep, i)
+            s.sync()
+    finally:
+        h.hipGraphExecDestroy(exe)
+        h.hipGraphDestroy(graph)
+        net.close()
         s.close()
