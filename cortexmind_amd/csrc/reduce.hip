@@ -278,9 +278,50 @@ __device__ __forceinline__ typename Op::T row_segment(const float *__restrict__ 
     return block_reduce<Op, kBlock>(r, lds);
 }
 
+// Whole rows of exactly NT * UNR float4 from 16-byte aligned bases (every
+// row aligned, no head or tail): one NT-thread workgroup per row, its loads
+// as straight-line code, then the folds in load order, the wave reductions
+// and one LDS exchange; thread 0 writes.  k_rows' one-segment form spent a
+// division, segment bounds, a loop test and head/tail code ahead of the
+// loads.  Measured A/B at C2's rows: sum 11.5 -> 11.3 us with 256 threads a
+// row, 11.2 with 128; max 11.7 -> 11.5 either way; argmax 12.0 -> 11.9 with
+// 256 but 12.1 with 128 (its (value, index) fold is twice the work), so the
+// 32-bit operators take 128 and the rest 256.
+template <class Op>
+constexpr int whole_block() { return sizeof(typename Op::T) == 4 ? 128 : 256; }
+template <class Op, int UNR>
+__global__ __launch_bounds__(whole_block<Op>()) void k_rows_whole(const float *__restrict__ x, size_t dim,
+                                                                   OutDesc out) {
+    using T = typename Op::T;
+    constexpr int NT = whole_block<Op>(), NW = NT / kWave;
+    __shared__ T lds[NW];
+    const int tid = threadIdx.x;
+    const float *__restrict__ xr = x + static_cast<size_t>(blockIdx.x) * dim;
+    float k = 0.0f;
+    if constexpr (Op::kShift) k = xr[0];
+    const float4 k4 = make_float4(k, k, k, k);
+    float4 v[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) v[u] = ld4_stream_at(xr, 16u * (tid + u * NT));
+    __builtin_amdgcn_sched_barrier(0);
+    T acc[4] = {Op::identity(), Op::identity(), Op::identity(), Op::identity()};
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], 4 * (tid + u * NT), 1, k4);
+    T r = Op::combine(Op::combine(acc[0], acc[1]), Op::combine(acc[2], acc[3]));
+    r = wave_reduce<Op>(r);
+    if ((tid & (kWave - 1)) == 0) lds[tid / kWave] = r;
+    __syncthreads();
+    if (tid == 0) {  // waves in order
+        T a = lds[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) a = Op::combine(a, lds[w]);
+        write_out<Op>(out, blockIdx.x, a);
+    }
+}
+
 // Reductions over the last axis: workgroup b reduces segment b % segs of
-// row b / segs.  MODE 0: one segment per row, written out directly (MODE 4:
-// the same for whole aligned rows of one load batch, straight-line).
+// row b / segs.  MODE 0: one segment per row, written out directly (whole
+// aligned rows of one load batch go to k_rows_whole instead).
 // MODE 1: segment partials to `part`; the last workgroup of a row (integer
 // ticket: one counter per row up to 32 segments, two levels beyond)
 // combines them in segment order.  MODE 2 (one row, 32-bit partials, at
@@ -316,35 +357,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
     __shared__ int flag;
     const int tid = threadIdx.x;
 
-    if constexpr (MODE == 4) {
-        // Whole rows of exactly UNR * kBlock float4 from a 16-byte aligned
-        // base (no head, no tail): straight-line loads, then the folds, the
-        // wave reductions and one LDS exchange; thread 0 writes.  MODE 0's
-        // arithmetic in the same order, so the same bits, without its
-        // segment bounds, loop test and head/tail code ahead of the loads
-        // (C2's row reductions, 11.5 -> 11.1 us in a stand-alone copy).
-        const float *__restrict__ xr = x + static_cast<size_t>(blockIdx.x) * dim;
-        float k = 0.0f;
-        if constexpr (Op::kShift) k = xr[0];
-        const float4 k4 = make_float4(k, k, k, k);
-        float4 v[UNR];
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) v[u] = ld4_stream_at(xr, 16u * (tid + u * kBlock));
-        __builtin_amdgcn_sched_barrier(0);
-        T acc[4] = {Op::identity(), Op::identity(), Op::identity(), Op::identity()};
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], 4 * (tid + u * kBlock), 1, k4);
-        T r = Op::combine(Op::combine(acc[0], acc[1]), Op::combine(acc[2], acc[3]));
-        r = wave_reduce<Op>(r);
-        if ((tid & (kWave - 1)) == 0) lds[tid / kWave] = r;
-        __syncthreads();
-        if (tid == 0) {  // block_reduce's order: waves 0, 1, 2, 3
-            T a = lds[0];
-#pragma unroll
-            for (int w = 1; w < kWavesPerBlock; ++w) a = Op::combine(a, lds[w]);
-            write_out<Op>(out, blockIdx.x, a);
-        }
-    } else if constexpr (MODE == 2 || MODE == 3) {
+    if constexpr (MODE == 2 || MODE == 3) {
         static_assert(sizeof(T) == 4, "tagged slots carry 32-bit partials");
         // MODE 3: the tag is one a graph replays (or the static region's),
         // so slots are emptied after use and given-up ones marked
@@ -700,9 +713,21 @@ int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t 
     T *part = nullptr;
     unsigned *counters = nullptr;
     TaggedSlots tg{nullptr, 0, 0, 0};
-    int mode = segs == 1 ? 0 : (rows == 1 && sizeof(T) == 4 && segs <= kMaxFlatSegs ? 2 : 1);
-    // whole aligned rows of one batch: every row starts 16-byte aligned
-    if (mode == 0 && aligned16(x) && dim % 4 == 0 && v4 == (unr8 ? 8u : 4u) * kBlock) mode = 4;
+    const int mode = segs == 1 ? 0 : (rows == 1 && sizeof(T) == 4 && segs <= kMaxFlatSegs ? 2 : 1);
+    // whole aligned rows of one batch (every row starts 16-byte aligned)
+    if (mode == 0 && aligned16(x) && dim % 4 == 0) {
+        const unsigned nr = static_cast<unsigned>(rows);
+        constexpr int nt = whole_block<Op>();
+#define CXM_WHOLE(U)                                                                                    \
+    if (v4 == static_cast<size_t>(U) * nt) {                                                            \
+        hipLaunchKernelGGL((k_rows_whole<Op, U>), dim3(nr), dim3(nt), 0, hs, x, dim, out);             \
+        return launch_status();                                                                         \
+    }
+        CXM_WHOLE(4)
+        CXM_WHOLE(8)
+        CXM_WHOLE(16)
+#undef CXM_WHOLE
+    }
     if (mode == 1) {
         const size_t nctr = segs <= kTicketGroups ? rows : rows * (kTicketGroups + 1);
         Scratch sc;
@@ -719,8 +744,7 @@ int run_rows(const float *x, size_t rows, size_t dim, OutDesc out, cxm_stream_t 
     const unsigned grid = mode == 2 ? nb + 1 : nb;
     const bool replayed = mode == 2 && tg.clear;  // MODE 3
 #define CXM_ROWS(U, M) launch_rows<Op, U, M>(grid, hs, x, dim, sg, seg4, part, counters, tg, out)
-    if (mode == 4) { if (unr8) CXM_ROWS(8, 4); else CXM_ROWS(4, 4); }
-    else if (mode == 0) { if (unr8) CXM_ROWS(8, 0); else CXM_ROWS(4, 0); }
+    if (mode == 0) { if (unr8) CXM_ROWS(8, 0); else CXM_ROWS(4, 0); }
     else if (mode == 1) { if (unr8) CXM_ROWS(8, 1); else CXM_ROWS(4, 1); }
     else if constexpr (sizeof(T) == 4) {
         if (replayed) { if (unr8) CXM_ROWS(8, 3); else CXM_ROWS(4, 3); }
