@@ -98,13 +98,13 @@ def wl_c2(E, D):
     ops = [
         Op("sum_global", "k_rows<SumOp,8,2>", rot(lambda b: R.sum(b, z1, n)), xb + 4),
         Op("mean_global", "k_rows<SumOp,8,2>", rot(lambda b: R.mean(b, z1, n)), xb + 4),
-        Op("sum_axis1", "k_rows<SumOp,4,0>", rot(lambda b: R.sum(b, zf, rows, cols, 1)), xb + 4 * rows),
-        Op("mean_axis1", "k_rows<SumOp,4,0>", rot(lambda b: R.mean(b, zf, rows, cols, 1)), xb + 4 * rows),
-        Op("max_axis1", "k_rows<MaxOp,4,0>", rot(lambda b: R.max(b, zf, rows, cols, 1)), xb + 4 * rows),
-        Op("argmax_axis1", "k_rows<ArgMaxOp,4,0>", rot(lambda b: R.argmax(b, zi, rows, cols, 1)), xb + 4 * rows),
-        Op("sum_axis0", "k_cols<SumOp,true,16,16,true>", rot(lambda b: R.sum(b, zf, 1, rows, cols)), xb + 4 * cols),
-        Op("mean_axis0", "k_cols<SumOp,true,16,16,true>", rot(lambda b: R.mean(b, zf, 1, rows, cols)), xb + 4 * cols),
-        Op("max_axis0", "k_cols<MaxColOp,true,16,16,true>", rot(lambda b: R.max(b, zf, 1, rows, cols)), xb + 4 * cols),
+        Op("sum_axis1", "k_rows_whole<SumOp,8>", rot(lambda b: R.sum(b, zf, rows, cols, 1)), xb + 4 * rows),
+        Op("mean_axis1", "k_rows_whole<SumOp,8>", rot(lambda b: R.mean(b, zf, rows, cols, 1)), xb + 4 * rows),
+        Op("max_axis1", "k_rows_whole<MaxOp,8>", rot(lambda b: R.max(b, zf, rows, cols, 1)), xb + 4 * rows),
+        Op("argmax_axis1", "k_rows_whole<ArgMaxOp,4>", rot(lambda b: R.argmax(b, zi, rows, cols, 1)), xb + 4 * rows),
+        Op("sum_axis0", "k_cols_whole<SumOp>", rot(lambda b: R.sum(b, zf, 1, rows, cols)), xb + 4 * cols),
+        Op("mean_axis0", "k_cols_whole<SumOp>", rot(lambda b: R.mean(b, zf, 1, rows, cols)), xb + 4 * cols),
+        Op("max_axis0", "k_cols_whole<MaxColOp>", rot(lambda b: R.max(b, zf, 1, rows, cols)), xb + 4 * cols),
         Op("argmax_axis0", "k_cols<ArgMaxOp,true,16,16,true>", rot(lambda b: R.argmax(b, zi, 1, rows, cols)), xb + 4 * cols),
     ]
     desc = {"workload": "C2 reductions fp32 [4096,4096] ~ U(-1,1)", "shape": [rows, cols],
@@ -223,10 +223,11 @@ def wl_more(E, D):
         kern = {"min": "MinOp", "argmin": "ArgMinOp", "norm1": "AbsSumOp", "norm2": "SqSumOp",
                 "var": "Pow2Op", "stdv": "Pow2Op"}[op]
         ops.append(Op(f"{op}_global", f"k_rows<{kern}>", rot(lambda b, fn=fn: fn(b, z1, n)), xb + 4))
-        ops.append(Op(f"{op}_axis1", f"k_rows<{kern}>", rot(lambda b, fn=fn, z=z: fn(b, z, rows, cols, 1)),
-                      xb + 4 * rows))
-        ops.append(Op(f"{op}_axis0", f"k_cols<{kern}>", rot(lambda b, fn=fn, z=z: fn(b, z, 1, rows, cols)),
-                      xb + 4 * cols))
+        wide = kern in ("ArgMinOp", "Pow2Op")  # 64-bit partials: whole rows 256 threads a row, general column kernel
+        ops.append(Op(f"{op}_axis1", f"k_rows_whole<{kern},{4 if wide else 8}>",
+                      rot(lambda b, fn=fn, z=z: fn(b, z, rows, cols, 1)), xb + 4 * rows))
+        ops.append(Op(f"{op}_axis0", f"k_cols<{kern}>" if wide else f"k_cols_whole<{kern}>",
+                      rot(lambda b, fn=fn, z=z: fn(b, z, 1, rows, cols)), xb + 4 * cols))
     # a flat sum of 2^24 + 3 floats from a base 4 bytes past 16-byte
     # alignment (the unaligned head and the ragged tail are folded in by the
     # first segment; the body still takes 128-bit loads)
