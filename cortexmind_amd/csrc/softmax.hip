@@ -370,9 +370,11 @@ constexpr size_t kXRowsMax = 8192;
 // workgroup stores at once.  Workgroups of row group g (of `groups`) sleep
 // g * quanta times 128 cycles before their first load, so the later groups'
 // loads fill the earlier groups' exchange gap.  Results do not depend on it.
-__device__ __forceinline__ void x_stagger(unsigned row, unsigned segs, unsigned groups, unsigned quanta) {
-    const unsigned rows = gridDim.x / segs;  // row < rows <= 8192, groups <= 16: 32-bit products
-    const unsigned n = row * groups / rows * quanta;
+// The group of a row is (row * gmul) >> 16 with gmul = groups * 2^16 / rows
+// from the host (a multiply, not a division, ahead of the loads; any split
+// of the rows into groups gives the same results).
+__device__ __forceinline__ void x_stagger(unsigned row, unsigned gmul, unsigned quanta) {
+    const unsigned n = ((row * gmul) >> 16) * quanta;  // row < 8192, gmul <= 2^20
     for (unsigned i = 0; i < n; ++i) __builtin_amdgcn_s_sleep(2);
 }
 
@@ -479,14 +481,14 @@ template <bool LOG>
 __global__ __launch_bounds__(kBlock) void k_sm_fwd_x(const float *__restrict__ x, float *__restrict__ y,
                                                      size_t cols, unsigned segs, unsigned *hdr,
                                                      unsigned long long *slots, unsigned limit,
-                                                     unsigned groups, unsigned quanta) {
+                                                     unsigned gmul, unsigned quanta) {
     constexpr int NV = kXNV;
     __shared__ float lds[kWavesPerBlock];
     __shared__ float part[2][kXMaxSegs];
     __shared__ unsigned long long s_miss;
-    const unsigned row = blockIdx.x / segs;
-    const unsigned seg = blockIdx.x - row * segs;
-    x_stagger(row, segs, groups, quanta);
+    // grid (segs, rows): no division ahead of the loads
+    const unsigned seg = blockIdx.x, row = blockIdx.y;
+    x_stagger(row, gmul, quanta);
     unsigned *h = hdr + row * kCtr;
     const unsigned tag = x_epoch(h) + 1;  // every wave: a load behind a branch would be waited for at its end
     const float *__restrict__ xr = x + static_cast<size_t>(row) * cols;
@@ -584,8 +586,7 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_x(const float *__restrict__ y
     __shared__ float lds[kWavesPerBlock];
     __shared__ float part[1][kXMaxSegs];
     __shared__ unsigned long long s_miss;
-    const unsigned row = blockIdx.x / segs;
-    const unsigned seg = blockIdx.x - row * segs;
+    const unsigned seg = blockIdx.x, row = blockIdx.y;  // grid (segs, rows)
     unsigned *h = hdr + row * kCtr;
     const unsigned tag = x_epoch(h) + 1;  // every wave: a load behind a branch would be waited for at its end
     const size_t rbase = static_cast<size_t>(row) * cols;
@@ -800,13 +801,15 @@ bool use_x(size_t rows, size_t cols) { return rows <= kXRowsMax && (cols + kXSeg
 // 20.0 us at pct 30 / 65 / 100) and starts at once.
 std::atomic<int> g_x_stagger_pct{65};
 
-void x_stagger_for(int pct, size_t rows, unsigned segs, size_t bytes_in, unsigned *groups, unsigned *quanta) {
-    *groups = 1;
+// groups as the multiplier gmul = groups * 2^16 / rows (see x_stagger)
+void x_stagger_for(int pct, size_t rows, unsigned segs, size_t bytes_in, unsigned *gmul, unsigned *quanta) {
+    *gmul = 0;
     *quanta = 0;
     if (pct <= 0 || rows < 2 || rows * segs > 1024) return;
-    *groups = rows < 16 ? static_cast<unsigned>(rows) : 16u;
+    const unsigned groups = rows < 16 ? static_cast<unsigned>(rows) : 16u;
+    *gmul = static_cast<unsigned>((static_cast<size_t>(groups) << 16) / rows);
     const double total = static_cast<double>(bytes_in) / 6.0e12 * (pct / 100.0) * 2.4e9 / 128.0;
-    *quanta = static_cast<unsigned>(total / (*groups - 1));
+    *quanta = static_cast<unsigned>(total / (groups - 1));
 }
 
 int sm_fwd_x(const float *x, float *y, size_t rows, size_t cols, int log_mode, cxm_stream_t st) {
@@ -814,7 +817,7 @@ int sm_fwd_x(const float *x, float *y, size_t rows, size_t cols, int log_mode, c
     Exchange xc;
     const int rc = get_exchange(st, rows, &xc);
     if (rc) return rc;
-    const dim3 grid(static_cast<unsigned>(rows * segs));
+    const dim3 grid(segs, static_cast<unsigned>(rows));  // rows <= kXRowsMax
     const unsigned lim = exchange_wait_limit();
     unsigned g, q;
     x_stagger_for(g_x_stagger_pct.load(std::memory_order_relaxed), rows, segs, rows * cols * sizeof(float), &g, &q);
@@ -833,7 +836,7 @@ int sm_bwd_x(const float *y, const float *dy, float *dx, size_t rows, size_t col
     Exchange xc;
     const int rc = get_exchange(st, rows, &xc);
     if (rc) return rc;
-    const dim3 grid(static_cast<unsigned>(rows * segs));
+    const dim3 grid(segs, static_cast<unsigned>(rows));  // rows <= kXRowsMax
     const unsigned lim = exchange_wait_limit();
     if (log_mode)
         hipLaunchKernelGGL(k_sm_bwd_x<true>, grid, dim3(kBlock), 0, hs(st), y, dy, dx, cols, segs, xc.hdr, xc.slots,
