@@ -811,12 +811,16 @@ struct ColPlan {
     size_t chunks;   // row chunks per column tile
 };
 
-// Default plan: 16-wave workgroups and about one workgroup per CU in
-// total (few chunks, so the last-workgroup combine reads few partials).
+// Default plan: 16-wave workgroups, about one per CU in total from 16
+// column tiles up and about 128 below (few chunks, so the last-workgroup
+// combine reads few partials).  Measured chunk sweeps (column sum, us):
+// [4096, 1024] 64 chunks 8.2, 32 chunks 7.0; [2048, 2048] 32: 7.2, 16: 6.5;
+// [8192, 512] 128: 11.0, 64: 8.1; [4096, 4096] 16: 13.1, 8: 14.8.
 ColPlan col_plan(size_t tiles, size_t dim) {
     ColPlan p{16, 1};
-    if (tiles < 256) {
-        size_t want = (256 + tiles - 1) / tiles;
+    const size_t target = tiles >= 16 ? 256 : 128;
+    if (tiles < target) {
+        size_t want = (target + tiles - 1) / tiles;
         const size_t max_chunks = (dim + 63) / 64;  // >= 4 rows per wave
         p.chunks = want < max_chunks ? want : max_chunks;
         if (p.chunks == 0) p.chunks = 1;
