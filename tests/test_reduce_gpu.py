@@ -150,6 +150,19 @@ def test_axis_shapes(hip, orc, sizes, op):
     check(op, x, sizes, orc)
 
 
+@pytest.mark.parametrize("sizes", [(64, 2048, 1), (32, 8192, 1), (16, 16384, 1), (2, 4096, 2048), (1, 4096, 512)],
+                         ids=lambda v: str(v))
+@pytest.mark.parametrize("op", ["sum", "mean", "max", "argmax"])
+def test_whole_row_and_chunk_forms(hip, orc, sizes, op):
+    """Shapes that take the straight-line kernels: whole aligned rows of one
+    load batch (2048, 8192 and 16384 floats: 4, 16 and -- for argmax's
+    256-thread rows -- 4 to 16 float4 a thread) and column chunks of exactly
+    256 rows over whole tiles, with two outer slices."""
+    o, d, i = sizes
+    x = SplitMix64(0x3A11 + o + d + i).uniform((o, d, i), -2.0, 2.0)
+    check(op, x, sizes, orc)
+
+
 def test_argmax_ties_first_index(hip, orc):
     x = np.zeros((6, 40), np.float32)
     x[1, [3, 17, 39]] = 5.0          # repeated maximum -> first one
