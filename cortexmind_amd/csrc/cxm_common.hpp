@@ -98,6 +98,18 @@ struct Epilogue {
 // C[M, N] = op(A) op(B) with the epilogue; the engine of cxm_gemm_f32.
 int gemm_ex(const float *A, const float *B, float *C, size_t M, size_t K, size_t N, int ta, int tb,
             const Epilogue &epi, cxm_stream_t s);
+// Two independent products (no operand of one is written by the other) as
+// one launch of the ring kernel when both take it at its whole-stage
+// instance with the same operand layouts (gemm.hip: k_gemm_ring_pair);
+// returns 1 when they do not, and the caller runs gemm_ex twice.
+struct GemmSpec {
+    const float *A, *B;
+    float *C;
+    size_t M, K, N;
+    int ta, tb;
+    Epilogue epi;
+};
+int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st);
 // b[j] = b[j] - lr * sum_i x[i, j] over x [rows, cols]: a bias gradient
 // (reduce::sum over axis 0) and its SGD step in one pass (reduce.hip).
 int colsum_sgd(const float *x, float *b, size_t rows, size_t cols, float lr, cxm_stream_t s);

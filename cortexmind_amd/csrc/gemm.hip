@@ -849,14 +849,12 @@ __device__ __forceinline__ void ring_last(const float *cur, const RingFrag &f0, 
 // steps and clamps, compiled into the one loop, moved the accumulators'
 // neighbours into AGPRs and slowed every whole-stage product by 2-3 us.
 template <bool KCA, bool KCB, bool TAIL>
-__global__ __launch_bounds__(kRingThreads) void k_gemm_ring(const float *__restrict__ A, const float *__restrict__ B,
-                                                            float *__restrict__ C, size_t M, size_t N, size_t K,
-                                                            unsigned tiles_n, unsigned splits, size_t kper,
-                                                            Epilogue epi, float *__restrict__ part,
-                                                            unsigned *__restrict__ counters) {
+__device__ __forceinline__ void ring_gemm(const float *__restrict__ A, const float *__restrict__ B,
+                                          float *__restrict__ C, size_t M, size_t N, size_t K, unsigned tiles_n,
+                                          unsigned splits, size_t kper, const Epilogue &epi,
+                                          float *__restrict__ part, unsigned *__restrict__ counters, unsigned wg) {
     __shared__ __attribute__((aligned(16))) float s0[2 * kRST], s1[2 * kRST], s2[2 * kRST], s3[2 * kRST];
     __shared__ int flag;
-    const unsigned wg = xcd_remap(blockIdx.x, gridDim.x);
     const unsigned tile = wg / splits;
     const unsigned split = wg - tile * splits;
     const size_t m0 = static_cast<size_t>(tile / tiles_n) * BM;
@@ -933,6 +931,41 @@ __global__ __launch_bounds__(kRingThreads) void k_gemm_ring(const float *__restr
 #undef CXM_RING_STEP
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
     gemm_epilogue<2, 2>(acc, C, M, N, m0, n0, tile, split, splits, wm, wn, lhi, l32, epi, part, counters, &flag);
+}
+
+template <bool KCA, bool KCB, bool TAIL>
+__global__ __launch_bounds__(kRingThreads) void k_gemm_ring(const float *__restrict__ A, const float *__restrict__ B,
+                                                            float *__restrict__ C, size_t M, size_t N, size_t K,
+                                                            unsigned tiles_n, unsigned splits, size_t kper,
+                                                            Epilogue epi, float *__restrict__ part,
+                                                            unsigned *__restrict__ counters) {
+    ring_gemm<KCA, KCB, TAIL>(A, B, C, M, N, K, tiles_n, splits, kper, epi, part, counters,
+                              xcd_remap(blockIdx.x, gridDim.x));
+}
+
+// Two independent ring products in one launch (the MLP's two weight
+// gradients): workgroups [0, g0.wgs) run the first, the rest the second,
+// each with its own tile order, split-K partials and tickets.  The second
+// product's workgroups start on the CUs the first one's release, with no
+// drain and refill of the chip between them.
+struct RingArgs {
+    const float *A, *B;
+    float *C;
+    size_t M, N, K;
+    unsigned tiles_n, splits;
+    size_t kper;
+    Epilogue epi;
+    float *part;
+    unsigned *counters;
+    unsigned wgs;  // workgroups of this product (a multiple of 8 for the XCD order, else dispatch order)
+};
+template <bool KCA, bool KCB>
+__global__ __launch_bounds__(kRingThreads) void k_gemm_ring_pair(RingArgs g0, RingArgs g1) {
+    const bool second = blockIdx.x >= g0.wgs;
+    const RingArgs &g = second ? g1 : g0;
+    const unsigned b = second ? blockIdx.x - g0.wgs : blockIdx.x;
+    ring_gemm<KCA, KCB, false>(g.A, g.B, g.C, g.M, g.N, g.K, g.tiles_n, g.splits, g.kper, g.epi, g.part, g.counters,
+                               xcd_remap(b, g.wgs));
 }
 
 // ------------------------------------------------ skinny products
@@ -1332,6 +1365,71 @@ int gemm_ex(const float *A, const float *B, float *C, size_t M, size_t K, size_t
     if (ta && !tb) return launch_t<true, false>(A, B, C, M, N, K, va, vb, grid, tn, sp, kper, epi, part, counters, s, variant);
     if (!ta && tb) return launch_t<false, true>(A, B, C, M, N, K, va, vb, grid, tn, sp, kper, epi, part, counters, s, variant);
     return launch_t<true, true>(A, B, C, M, N, K, va, vb, grid, tn, sp, kper, epi, part, counters, s, variant);
+}
+
+namespace {
+
+// The split plan gemm_ex uses for a ring product (see above): the ring at
+// its whole-stage instance, the split count and each split's k range.
+// Returns false when gemm_ex would not run this shape on that instance.
+bool ring_plan(const float *A, const float *B, size_t M, size_t K, size_t N, int ta, int tb, size_t *tiles,
+               size_t *tiles_n, size_t *splits, size_t *kper) {
+    if (M == 0 || N == 0 || K == 0 || K % (4 * kRBK) != 0 || (ta && tb)) return false;
+    if (N <= kThin || K <= kThin) return false;  // thin kernels
+    const bool ring_ok = K % 8 == 0 && aligned16(A) && aligned16(B) && M >= 4 && N >= 4 &&
+                         (!ta || M % 4 == 0) && (tb || N % 4 == 0);
+    const size_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN, t = tm * tn;
+    size_t sp = 1;
+    if (t < 192 && K >= 512) {
+        sp = 256 / t;
+        const size_t max_splits = K / 256;
+        if (sp > max_splits) sp = max_splits;
+        if (sp < 1) sp = 1;
+    }
+    if (gemm_variant(ta, tb, static_cast<unsigned>(t * sp), ring_ok) != 7) return false;
+    size_t kp = (K + sp - 1) / sp;
+    kp = (kp + 4 * kRBK - 1) / (4 * kRBK) * (4 * kRBK);
+    sp = (K + kp - 1) / kp;
+    if (kp % (4 * kRBK) != 0 || t * sp > 0x7fffffffu) return false;
+    *tiles = t;
+    *tiles_n = tn;
+    *splits = sp;
+    *kper = kp;
+    return true;
+}
+
+}  // namespace
+
+int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st) {
+    size_t ta_t, ta_n, ta_s, ta_k, tb_t, tb_n, tb_s, tb_k;
+    if (!a.A || !a.B || !a.C || !b.A || !b.B || !b.C || a.ta != b.ta || a.tb != b.tb) return 1;
+    if (a.epi.act != CXM_ACT_NONE && a.epi.act != CXM_ACT_RELU) return 1;
+    if (b.epi.act != CXM_ACT_NONE && b.epi.act != CXM_ACT_RELU) return 1;
+    if (!ring_plan(a.A, a.B, a.M, a.K, a.N, a.ta, a.tb, &ta_t, &ta_n, &ta_s, &ta_k)) return 1;
+    if (!ring_plan(b.A, b.B, b.M, b.K, b.N, b.ta, b.tb, &tb_t, &tb_n, &tb_s, &tb_k)) return 1;
+    const size_t wa = ta_t * ta_s, wb = tb_t * tb_s;
+    if (wa + wb > 0x7fffffffu) return 1;
+    float *part = nullptr;
+    unsigned *counters = nullptr;
+    const size_t pa = ta_s > 1 ? ta_t * ta_s * BM * BN : 0, pb = tb_s > 1 ? tb_t * tb_s * BM * BN : 0;
+    if (pa + pb) {
+        Workspace ws;
+        const int rc = get_workspace(st, ta_t + tb_t, (pa + pb) * sizeof(float), &ws);
+        if (rc) return rc;
+        part = static_cast<float *>(ws.scratch);
+        counters = ws.counters;
+    }
+    const RingArgs ga{a.A, a.B, a.C, a.M, a.N, a.K, static_cast<unsigned>(ta_n), static_cast<unsigned>(ta_s), ta_k,
+                      a.epi, part, counters, static_cast<unsigned>(wa)};
+    const RingArgs gb{b.A, b.B, b.C, b.M, b.N, b.K, static_cast<unsigned>(tb_n), static_cast<unsigned>(tb_s), tb_k,
+                      b.epi, part ? part + pa : nullptr, counters ? ctr(counters, ta_t) : nullptr,
+                      static_cast<unsigned>(wb)};
+    hipStream_t s = reinterpret_cast<hipStream_t>(st);
+    const dim3 grid(static_cast<unsigned>(wa + wb));
+    if (!a.ta && !a.tb) hipLaunchKernelGGL((k_gemm_ring_pair<true, false>), grid, dim3(kRingThreads), 0, s, ga, gb);
+    else if (a.ta && !a.tb) hipLaunchKernelGGL((k_gemm_ring_pair<false, false>), grid, dim3(kRingThreads), 0, s, ga, gb);
+    else hipLaunchKernelGGL((k_gemm_ring_pair<true, true>), grid, dim3(kRingThreads), 0, s, ga, gb);
+    return launch_status();
 }
 
 }  // namespace cxm

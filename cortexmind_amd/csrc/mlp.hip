@@ -413,12 +413,24 @@ int cxm_mlp3_step_f32(cxm_mlp3 *h, const float *x, const int32_t *labels, float 
         CXM_TRY(cxm::gemm_ex(h->h2, h->dl, w3, d2, B, d3, 1, 0, sgd, s));
         CXM_TRY(cxm::colsum_sgd(h->dl, b3, B, d3, lr, s));
     }
-    // layer 2
+    // layer 2: dX first (reads W2)
     CXM_TRY(cxm::gemm_ex(h->dh2, w2, h->dh1, B, d2, d1, 0, 1, Epilogue{nullptr, h->h1, CXM_ACT_NONE, 0, 0.0f}, s));
-    CXM_TRY(cxm::gemm_ex(h->h1, h->dh2, w2, d1, B, d2, 1, 0, sgd, s));
     if (!h->fused_head) CXM_TRY(cxm::colsum_sgd(h->dh2, b2, B, d2, lr, s));
-    // layer 1
-    CXM_TRY(cxm::gemm_ex(x, h->dh1, w1, d0, B, d1, 1, 0, sgd, s));
+    // the two weight gradients with their SGD steps, W2 -= lr h1^T dH2 and
+    // W1 -= lr x^T dH1: independent, so one launch where both take the ring
+    // (the second's workgroups fill the CUs the first releases); else in turn
+    {
+        const cxm::GemmSpec g2{h->h1, h->dh2, w2, d1, B, d2, 1, 0, sgd};
+        const cxm::GemmSpec g1{x, h->dh1, w1, d0, B, d1, 1, 0, sgd};
+        rc = cxm::gemm_ex_pair(g2, g1, s);
+        if (rc == 1) {
+            CXM_TRY(cxm::gemm_ex(h->h1, h->dh2, w2, d1, B, d2, 1, 0, sgd, s));
+            CXM_TRY(cxm::gemm_ex(x, h->dh1, w1, d0, B, d1, 1, 0, sgd, s));
+        } else if (rc) {
+            return rc;
+        }
+    }
+    // layer 1 bias
     CXM_TRY(cxm::colsum_sgd(h->dh1, b1, B, d1, lr, s));
 #undef CXM_TRY
     return CXM_OK;
