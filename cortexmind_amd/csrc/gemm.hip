@@ -1398,6 +1398,20 @@ bool ring_plan(const float *A, const float *B, size_t M, size_t K, size_t N, int
     return true;
 }
 
+// Re-plans a ring product's K split at `sp` splits: each split's k range a
+// whole number of ring stages.
+bool ring_resplit(size_t K, size_t sp, size_t *splits, size_t *kper) {
+    size_t kp = (K + sp - 1) / sp;
+    kp = (kp + 4 * kRBK - 1) / (4 * kRBK) * (4 * kRBK);
+    if (kp == 0 || kp % (4 * kRBK) != 0) return false;
+    *kper = kp;
+    *splits = (K + kp - 1) / kp;
+    return true;
+}
+
+// CUs of the part: one ring workgroup (128 KiB of LDS) per CU.
+constexpr size_t kRingCUs = 256;
+
 }  // namespace
 
 int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st) {
@@ -1407,6 +1421,13 @@ int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st) {
     if (b.epi.act != CXM_ACT_NONE && b.epi.act != CXM_ACT_RELU) return 1;
     if (!ring_plan(a.A, a.B, a.M, a.K, a.N, a.ta, a.tb, &ta_t, &ta_n, &ta_s, &ta_k)) return 1;
     if (!ring_plan(b.A, b.B, b.M, b.K, b.N, b.ta, b.tb, &tb_t, &tb_n, &tb_s, &tb_k)) return 1;
+    // Each plan alone fills the chip; together they would run as two rounds
+    // of workgroups, each paying the ring's fill and epilogue.  One split
+    // count for both that keeps the pair within one round instead.
+    if (ta_t * ta_s + tb_t * tb_s > kRingCUs) {
+        const size_t sp = std::max<size_t>(1, kRingCUs / (ta_t + tb_t));
+        if (!ring_resplit(a.K, sp, &ta_s, &ta_k) || !ring_resplit(b.K, sp, &tb_s, &tb_k)) return 1;
+    }
     const size_t wa = ta_t * ta_s, wb = tb_t * tb_s;
     if (wa + wb > 0x7fffffffu) return 1;
     float *part = nullptr;
