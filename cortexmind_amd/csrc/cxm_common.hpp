@@ -185,6 +185,19 @@ __device__ __forceinline__ void lds_load16(const void *gsrc, const void *lds) {
     asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gsrc), "{m0}"(a) : "memory");
 }
 
+// The same load from a wave-uniform base (an SGPR pair) plus a 32-bit
+// per-lane byte offset (the saddr form): the lane's address costs no 64-bit
+// vector arithmetic.
+// `lds` is the LDS byte address (lds_addr), wave-uniform.
+__device__ __forceinline__ void lds_load16_at(const void *base, unsigned off, unsigned lds) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+// LDS byte address of a __shared__ location, as a wave-uniform value.
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+    return __builtin_amdgcn_readfirstlane(
+        static_cast<unsigned>(reinterpret_cast<size_t>((const __attribute__((address_space(3))) void *)p)));
+}
+
 // Barrier of an LDS ring filled by lds_load16: this wave waits until at
 // most PENDING of its global loads are outstanding (loads retire in order,
 // so every older fill has landed in LDS) and for its own LDS reads, then

@@ -732,6 +732,16 @@ constexpr int kRBK = 32;                    // k per stage
 constexpr int kRST = BM * kRBK;             // floats per operand stage
 constexpr int kRPS = 2 * (kRST / 4 / kRingThreads);  // lds_load16 per wave per stage (A and B)
 
+// Shapes the ring takes: whole 8-k blocks; a partial last M or N tile is
+// clamped, which needs the [K, M] / [K, N] storage's row length a multiple
+// of 4; a lane's offset within a stage (at most 127 rows, or 31 k rows, of
+// the stored operand) fits 32 bits.
+inline bool ring_shape_ok(const float *A, const float *B, size_t M, size_t K, size_t N, int ta, int tb) {
+    constexpr size_t kMaxLd = size_t(1) << 23;
+    return K % 8 == 0 && aligned16(A) && aligned16(B) && M >= 4 && N >= 4 && (!ta || M % 4 == 0) &&
+           (tb || N % 4 == 0) && M < kMaxLd && N < kMaxLd && K < kMaxLd;
+}
+
 __device__ __forceinline__ int rk_c(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int rk_m(int k) { return 8 * ((k >> 2) & 1); }
 
@@ -760,6 +770,61 @@ __device__ __forceinline__ void ring_fill(const float *__restrict__ X, size_t r0
             const size_t gc = r0 + 4 * (p ^ rk_m(kr)), gk = k0 + kr;
             lds_load16(X + (!TAIL || gk < klast ? gk : klast) * ld + (gc < rlast ? gc : rlast), stage + kb * BM);
         }
+    }
+}
+
+// ring_fill for a stage with no k clamp, as base + per-lane offset: the
+// stage's base is X + r0 ld + k0 (k-contiguous) or X + k0 ld + r0, uniform
+// across the workgroup, and lane offsets (ring_offsets) stay fixed for the
+// whole K loop.  Same addresses, same LDS layout as ring_fill.
+struct RingOffs {
+    unsigned o[4];
+};
+template <bool KC>
+__device__ __forceinline__ RingOffs ring_offsets(size_t r0, size_t ld, size_t rlast) {
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    RingOffs f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        if constexpr (KC) {
+            const int row = w * 32 + s * 8 + (lane >> 3), p = lane & 7;
+            const size_t gr = r0 + row < rlast ? r0 + row : rlast;
+            f.o[s] = static_cast<unsigned>(((gr - r0) * ld + 4 * (p ^ rk_c(row))) * sizeof(float));
+        } else {
+            const int kr = w * 8 + s * 2 + (lane >> 5), p = lane & 31;
+            const size_t gc = r0 + 4 * (p ^ rk_m(kr));
+            f.o[s] = static_cast<unsigned>((kr * ld + ((gc < rlast ? gc : rlast) - r0)) * sizeof(float));
+        }
+    }
+    return f;
+}
+template <bool KC>
+__device__ __forceinline__ void ring_fill_at(const float *__restrict__ X, size_t r0, size_t k0, size_t ld,
+                                             const RingOffs &f, float *stage) {
+    const unsigned w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const float *base = KC ? X + r0 * ld + k0 : X + k0 * ld + r0;
+    // this wave's first LDS destination; each load fills the next 1 KiB
+    const unsigned l0 = lds_addr(stage) + (KC ? w * 32 * kRBK : w * 8 * BM) * sizeof(float);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) lds_load16_at(base, f.o[s], l0 + s * kWave * 16);
+}
+
+// Fills stage `st` (A at +0, B at +kRST) with the 32 k from kf: through
+// the offsets when the stage lies inside K (always without TAIL), else
+// with ring_fill's k clamp (ka, kb: the last k group or row of A and B).
+template <bool KCA, bool KCB, bool TAIL>
+__device__ __forceinline__ void ring_fill_any(const float *__restrict__ A, const float *__restrict__ B, size_t lda,
+                                              size_t ldb, size_t m0, size_t n0, size_t ra, size_t rb, size_t ka,
+                                              size_t kb, size_t kf, const RingOffs &oa, const RingOffs &ob,
+                                              float *st) {
+    // the stage's last k, kf + 31, inside K: for A [M,K] ka = K - 4 (the
+    // last 4-k group's start), for A [K,M] ka = K - 1
+    if (!TAIL || kf + kRBK - (KCA ? 4 : 1) <= ka) {
+        ring_fill_at<KCA>(A, m0, kf, lda, oa, st);
+        ring_fill_at<KCB>(B, n0, kf, ldb, ob, st + kRST);
+    } else {
+        ring_fill<KCA, TAIL>(A, m0, kf, lda, ra, ka, st);
+        ring_fill<KCB, TAIL>(B, n0, kf, ldb, rb, kb, st + kRST);
     }
 }
 
@@ -815,7 +880,8 @@ template <bool KCA, bool KCB, bool TAIL>
 __device__ __forceinline__ void ring_step(const float *__restrict__ A, const float *__restrict__ B, size_t lda,
                                           size_t ldb, size_t m0, size_t n0, size_t ra, size_t rb, size_t ka,
                                           size_t kb, size_t kf, float *cur, const float *nxt, RingFrag &f0,
-                                          floatx16 (&acc)[2][2], int wm, int wn, int l32, int lhi) {
+                                          floatx16 (&acc)[2][2], int wm, int wn, int l32, int lhi,
+                                          const RingOffs &oa, const RingOffs &ob) {
     RingFrag f1, f2;
     ring_frags<KCA, KCB>(cur, 1, wm, wn, l32, lhi, f1);
     ring_block<KCA, KCB>(f0, acc);
@@ -825,8 +891,7 @@ __device__ __forceinline__ void ring_step(const float *__restrict__ A, const flo
     ring_block<KCA, KCB>(f2, acc);
     ring_barrier<2 * kRPS>();  // tile t+1 landed; every wave done reading cur
     ring_frags<KCA, KCB>(nxt, 0, wm, wn, l32, lhi, f0);
-    ring_fill<KCA, TAIL>(A, m0, kf, lda, ra, ka, cur);
-    ring_fill<KCB, TAIL>(B, n0, kf, ldb, rb, kb, cur + kRST);
+    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kf, oa, ob, cur);
     ring_block<KCA, KCB>(f1, acc);
 }
 
@@ -880,19 +945,17 @@ __device__ __forceinline__ void ring_gemm(const float *__restrict__ A, const flo
     // into stages whose fragments go unused.
     const size_t len = kend - kbeg, T = (len + kRBK - 1) / kRBK;
     auto kt = [&](size_t t) { return kbeg + (t < T ? t : T - 1) * kRBK; };
-    ring_fill<KCA, TAIL>(A, m0, kt(0), lda, ra, ka, s0);
-    ring_fill<KCB, TAIL>(B, n0, kt(0), ldb, rb, kb, s0 + kRST);
-    ring_fill<KCA, TAIL>(A, m0, kt(1), lda, ra, ka, s1);
-    ring_fill<KCB, TAIL>(B, n0, kt(1), ldb, rb, kb, s1 + kRST);
-    ring_fill<KCA, TAIL>(A, m0, kt(2), lda, ra, ka, s2);
-    ring_fill<KCB, TAIL>(B, n0, kt(2), ldb, rb, kb, s2 + kRST);
-    ring_fill<KCA, TAIL>(A, m0, kt(3), lda, ra, ka, s3);
-    ring_fill<KCB, TAIL>(B, n0, kt(3), ldb, rb, kb, s3 + kRST);
+    const RingOffs oa = ring_offsets<KCA>(m0, lda, ra), ob = ring_offsets<KCB>(n0, ldb, rb);
+    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kt(0), oa, ob, s0);
+    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kt(1), oa, ob, s1);
+    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kt(2), oa, ob, s2);
+    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kt(3), oa, ob, s3);
     ring_barrier<3 * kRPS>();
     RingFrag f0;
     ring_frags<KCA, KCB>(s0, 0, wm, wn, l32, lhi, f0);
 #define CXM_RING_STEP(T4, CUR, NXT) \
-    ring_step<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kt(T4), CUR, NXT, f0, acc, wm, wn, l32, lhi)
+    ring_step<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kt(T4), CUR, NXT, f0, acc, wm, wn, l32, lhi, \
+                              oa, ob)
     if constexpr (!TAIL) {
         for (size_t t = 0; t < T; t += 4) {  // T is a multiple of 4
             CXM_RING_STEP(t + 4, s0, s1);
@@ -1337,9 +1400,9 @@ int gemm_ex(const float *A, const float *B, float *C, size_t M, size_t K, size_t
     // a split's k range is a whole number of the kernel's k steps (the
     // ring's: four stages of 32)
     // the ring: whole 8-k blocks; a partial last M or N tile is clamped,
-    // which needs the [K, M] / [K, N] storage's row length a multiple of 4
-    const bool ring_ok = K % 8 == 0 && aligned16(A) && aligned16(B) && M >= 4 && N >= 4 &&
-                         (!ta || M % 4 == 0) && (tb || N % 4 == 0);
+    // which needs the [K, M] / [K, N] storage's row length a multiple of 4;
+    // its lanes address a stage with 32-bit byte offsets (ring_offsets)
+    const bool ring_ok = ring_shape_ok(A, B, M, K, N, ta, tb);
     const int variant = gemm_variant(ta, tb, static_cast<unsigned>(tiles * splits), ring_ok);
     const size_t kstep = variant == 7 ? 4 * kRBK : (variant == 2 || variant == 4) ? 64 : BK;
     size_t kper = (K + splits - 1) / splits;
@@ -1376,8 +1439,7 @@ bool ring_plan(const float *A, const float *B, size_t M, size_t K, size_t N, int
                size_t *tiles_n, size_t *splits, size_t *kper) {
     if (M == 0 || N == 0 || K == 0 || K % (4 * kRBK) != 0 || (ta && tb)) return false;
     if (N <= kThin || K <= kThin) return false;  // thin kernels
-    const bool ring_ok = K % 8 == 0 && aligned16(A) && aligned16(B) && M >= 4 && N >= 4 &&
-                         (!ta || M % 4 == 0) && (tb || N % 4 == 0);
+    const bool ring_ok = ring_shape_ok(A, B, M, K, N, ta, tb);
     const size_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN, t = tm * tn;
     size_t sp = 1;
     if (t < 192 && K >= 512) {
