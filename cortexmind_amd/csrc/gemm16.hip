@@ -576,41 +576,55 @@ __device__ __forceinline__ int noff(int r, int n) {
     return r * TM + ((((n >> 3) ^ (4 * (r & 3)))) << 3) + (n & 7);
 }
 
-// Loads one TM x 32 stage of X (k-contiguous, row stride Kd) at rows r0..,
-// k0..: each wave fills TM/4 rows, 16 per instruction (lane L: row L/4, LDS
-// group L%4, global group (L%4) ^ key).
+// Stage fills.  A TM x 32 stage of X k-contiguous (row stride Kd) at rows
+// r0.., k0..: each wave fills TM/4 rows, 16 per instruction (lane L: row
+// L/4, LDS group L%4, global group (L%4) ^ key).  A 32 x TM stage of B
+// stored [K,N] (row stride N) at k rows k0.., columns n0..: each wave
+// fills 8 rows; an instruction covers 1 KiB, i.e. 64 / (TM/8) rows (lane
+// L: row L / (TM/8), LDS chunk L % (TM/8), global chunk
+// (L % (TM/8)) ^ 4*(row % 4)).  Each load reads from a base uniform across
+// the workgroup (X + r0 Kd + k0, or B + k0 N + n0) plus a 32-bit lane
+// offset fixed for the whole K loop (RingOffs16), into an LDS destination
+// computed on the scalar unit: no 64-bit vector address arithmetic per load.
 template <int TM>
-__device__ __forceinline__ void ring_issue(const uint16_t *__restrict__ X, size_t r0, size_t k0, size_t Kd,
-                                           uint16_t *stage) {
+struct RingOffs16 {
+    unsigned o[Ring<TM>::ISSUES];
+};
+template <int TM>
+__device__ __forceinline__ RingOffs16<TM> ring_offs_k(size_t Kd) {
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
     const int rr = lane >> 2, p = lane & 3;
+    RingOffs16<TM> f;
 #pragma unroll
     for (int s = 0; s < Ring<TM>::ISSUES; ++s) {
-        const int rb = w * (TM / 4) + s * 16;
-        const int row = rb + rr;
-        const uint16_t *src = X + (r0 + row) * Kd + k0 + 8 * (p ^ rkey(row));
-        lds_load16(src, stage + rb * kR_BK);
+        const int row = w * (TM / 4) + s * 16 + rr;
+        f.o[s] = static_cast<unsigned>((row * Kd + 8 * (p ^ rkey(row))) * sizeof(uint16_t));
     }
+    return f;
 }
-
-// Loads one 32 x TM stage of B stored [K,N] (row stride N) at k rows k0..,
-// columns n0..: each wave fills 8 rows; an instruction covers 1 KiB, i.e.
-// 64 / (TM/8) rows (lane L: row L / (TM/8), LDS chunk L % (TM/8), global
-// chunk (L % (TM/8)) ^ 4*(row % 4)).
 template <int TM>
-__device__ __forceinline__ void ring_issue_n(const uint16_t *__restrict__ B, size_t k0, size_t n0, size_t N,
-                                             uint16_t *stage) {
-    constexpr int CPR = TM / 8;      // 16-byte chunks per row
-    constexpr int RPI = kWave / CPR;  // rows per instruction
+__device__ __forceinline__ RingOffs16<TM> ring_offs_n(size_t N) {
+    constexpr int CPR = TM / 8, RPI = kWave / CPR;
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
     const int rr = lane / CPR, p = lane % CPR;
+    RingOffs16<TM> f;
 #pragma unroll
     for (int s = 0; s < Ring<TM>::ISSUES; ++s) {
-        const int rb = w * 8 + s * RPI;
-        const int row = rb + rr;
-        const uint16_t *src = B + (k0 + row) * N + n0 + 8 * (p ^ (4 * (row & 3)));
-        lds_load16(src, stage + rb * TM);
+        const int row = w * 8 + s * RPI + rr;
+        f.o[s] = static_cast<unsigned>((row * N + 8 * (p ^ (4 * (row & 3)))) * sizeof(uint16_t));
     }
+    return f;
+}
+// k-contiguous stage (KC) at rows r0.., k0..; else a [K,N] stage at k rows
+// k0.., columns r0..
+template <int TM, bool KC>
+__device__ __forceinline__ void ring_issue_at(const uint16_t *__restrict__ X, size_t r0, size_t k0, size_t ld,
+                                              const RingOffs16<TM> &f, uint16_t *stage) {
+    const unsigned w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint16_t *base = KC ? X + r0 * ld + k0 : X + k0 * ld + r0;
+    const unsigned l0 = lds_addr(stage) + (KC ? w * (TM / 4) * kR_BK : w * 8 * TM) * sizeof(uint16_t);
+#pragma unroll
+    for (int s = 0; s < Ring<TM>::ISSUES; ++s) lds_load16_at(base, f.o[s], l0 + s * kWave * 16);
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -684,9 +698,9 @@ __device__ __forceinline__ void ring_interleave() {
 // Fills a B stage: k-contiguous (B^T [N,K], rows n0..) or [K,N] (k rows k0..).
 template <int TM, bool KB>
 __device__ __forceinline__ void ring_issue_b(const uint16_t *__restrict__ B, size_t n0, size_t kf, size_t K, size_t N,
-                                             uint16_t *stage) {
-    if constexpr (KB) ring_issue<TM>(B, n0, kf, K, stage);
-    else ring_issue_n<TM>(B, kf, n0, N, stage);
+                                             const RingOffs16<TM> &ob, uint16_t *stage) {
+    if constexpr (KB) ring_issue_at<TM, true>(B, n0, kf, K, ob, stage);
+    else ring_issue_at<TM, false>(B, n0, kf, N, ob, stage);
 }
 
 // Step t on stage cur (A tile at +0, B tile at +TILE, tile t); nxt holds
@@ -697,7 +711,7 @@ __device__ __forceinline__ void ring_step(const uint16_t *__restrict__ A, const 
                                           size_t N, size_t m0, size_t n0, size_t kf, uint16_t *cur,
                                           const uint16_t *nxt, u32x4 (&fa)[Ring<TM>::NB], u32x4 (&fb)[Ring<TM>::NB],
                                           f32x16 (&acc)[Ring<TM>::NB][Ring<TM>::NB], int wm, int wn, int l32,
-                                          int lhi) {
+                                          int lhi, const RingOffs16<TM> &oa, const RingOffs16<TM> &ob) {
     constexpr int NB = Ring<TM>::NB, TILE = Ring<TM>::TILE;
     u32x4 ga[NB], gb[NB];
     ring_frags<TM, KB>(cur, cur + TILE, 1, wm, wn, l32, lhi, ga, gb);  // block 1, during block 0's MFMAs
@@ -705,8 +719,8 @@ __device__ __forceinline__ void ring_step(const uint16_t *__restrict__ A, const 
     ring_interleave<TM, KB>();
     ring_barrier<2 * Ring<TM>::PER_STAGE>();  // tile t+1 has landed; tiles t+2, t+3 may be in flight
     ring_frags<TM, KB>(nxt, nxt + TILE, 0, wm, wn, l32, lhi, fa, fb);  // next step's block 0
-    ring_issue<TM>(A, m0, kf, K, cur);
-    ring_issue_b<TM, KB>(B, n0, kf, K, N, cur + TILE);
+    ring_issue_at<TM, true>(A, m0, kf, K, oa, cur);
+    ring_issue_b<TM, KB>(B, n0, kf, K, N, ob, cur + TILE);
     ring_mfma<DT, NB>(ga, gb, acc);
     ring_interleave<TM, KB>();
     __builtin_amdgcn_sched_group_barrier(0x020, Ring<TM>::PER_STAGE, 0);
@@ -757,22 +771,23 @@ __global__ __launch_bounds__(kHThreads) void k_gemm16_ring(const uint16_t *__res
     // into stages whose fragments are not used.
     const size_t T = K / kR_BK;
     auto kt = [&](size_t t) { return (t < T ? t : T - 1) * kR_BK; };
-    ring_issue<TM>(A, m0, kt(0), K, s0);
-    ring_issue_b<TM, KB>(B, n0, kt(0), K, N, s0 + TILE);
-    ring_issue<TM>(A, m0, kt(1), K, s1);
-    ring_issue_b<TM, KB>(B, n0, kt(1), K, N, s1 + TILE);
-    ring_issue<TM>(A, m0, kt(2), K, s2);
-    ring_issue_b<TM, KB>(B, n0, kt(2), K, N, s2 + TILE);
-    ring_issue<TM>(A, m0, kt(3), K, s3);
-    ring_issue_b<TM, KB>(B, n0, kt(3), K, N, s3 + TILE);
+    const RingOffs16<TM> oa = ring_offs_k<TM>(K), ob = KB ? ring_offs_k<TM>(K) : ring_offs_n<TM>(N);
+    ring_issue_at<TM, true>(A, m0, kt(0), K, oa, s0);
+    ring_issue_b<TM, KB>(B, n0, kt(0), K, N, ob, s0 + TILE);
+    ring_issue_at<TM, true>(A, m0, kt(1), K, oa, s1);
+    ring_issue_b<TM, KB>(B, n0, kt(1), K, N, ob, s1 + TILE);
+    ring_issue_at<TM, true>(A, m0, kt(2), K, oa, s2);
+    ring_issue_b<TM, KB>(B, n0, kt(2), K, N, ob, s2 + TILE);
+    ring_issue_at<TM, true>(A, m0, kt(3), K, oa, s3);
+    ring_issue_b<TM, KB>(B, n0, kt(3), K, N, ob, s3 + TILE);
     ring_barrier<3 * PS>();
     u32x4 fa[NB], fb[NB];
     ring_frags<TM, KB>(s0, s0 + TILE, 0, wm, wn, l32, lhi, fa, fb);
     for (size_t t = 0; t < T; t += 4) {
-        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 4), s0, s1, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 5), s1, s2, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 6), s2, s3, fa, fb, acc, wm, wn, l32, lhi);
-        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 7), s3, s0, fa, fb, acc, wm, wn, l32, lhi);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 4), s0, s1, fa, fb, acc, wm, wn, l32, lhi, oa, ob);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 5), s1, s2, fa, fb, acc, wm, wn, l32, lhi, oa, ob);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 6), s2, s3, fa, fb, acc, wm, wn, l32, lhi, oa, ob);
+        ring_step<DT, TM, KB>(A, B, K, N, m0, n0, kt(t + 7), s3, s0, fa, fb, acc, wm, wn, l32, lhi, oa, ob);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
 
@@ -927,7 +942,9 @@ int gemm16(const uint16_t *A, const uint16_t *B, uint16_t *C, size_t M, size_t K
     const bool vb = aligned16(B) && (tb ? K % 8 == 0 : N % 8 == 0);
     hipStream_t s = hs(st);
     const size_t big_tiles = ((M + kG_BM - 1) / kG_BM) * ((N + kG_BN - 1) / kG_BN);
-    const bool al = aligned16(A) && aligned16(B) && aligned16(C) && K % (4 * kR_BK) == 0;
+    // (the ring's lane offsets within a stage are 32-bit: K, N < 2^23)
+    const bool al = aligned16(A) && aligned16(B) && aligned16(C) && K % (4 * kR_BK) == 0 &&
+                    K < (size_t(1) << 23) && N < (size_t(1) << 23);
     const bool ring256 = al && M % 256 == 0 && N % 256 == 0;
     const bool ring128 = al && M % 128 == 0 && N % 128 == 0;
     int kernel = big_tiles >= 128 ? (ring256 ? 2 : 1) : (ring128 ? 3 : 0);
