@@ -745,43 +745,26 @@ inline bool ring_shape_ok(const float *A, const float *B, size_t M, size_t K, si
 __device__ __forceinline__ int rk_c(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int rk_m(int k) { return 8 * ((k >> 2) & 1); }
 
-// Fills one operand stage: k-contiguous X[r][k] (ld = K) at rows r0..,
-// k0..: eight rows of 32 floats per instruction; else X[k][r] (ld = row
-// length) at k rows k0.., columns r0..: two k rows of 128 floats each.
-// `rlast` clamps the global row (KC) or 4-column group start (otherwise) of
-// a partial last tile to the operand's last one: rows or columns past the
-// operand's end load duplicates, whose products land only in accumulator
-// rows or columns that the epilogue does not store.  `klast` clamps k the
-// same way (the last 4-k group start for KC, else the last k row): a
-// stage that runs past K loads duplicates into 8-k blocks that are never
+// Stage fills.  A k-contiguous operand X[r][k] (ld = K) fills eight rows
+// of 32 floats per instruction; the other, X[k][r] (ld = row length), two
+// k rows of 128 floats.  Each load reads from a base uniform across the
+// workgroup, X + r0 ld + k0 (k-contiguous) or X + k0 ld + r0, plus a
+// 32-bit per-lane offset that stays fixed for the whole K loop, into an
+// LDS destination computed on the scalar unit: no 64-bit vector address
+// arithmetic per load.  The offsets clamp the row (k-contiguous) or
+// 4-column group start (otherwise) of a partial last tile to the
+// operand's last one (rlast): rows or columns past the operand's end load
+// duplicates, whose products land only in accumulator rows or columns
+// that the epilogue does not store.  Offsets for a stage with kv < 32
+// valid k (the last tile of a split whose k range is not a multiple of
+// 32) clamp k the same way, to the last 4-k group start or the last k
+// row: that stage loads duplicates into 8-k blocks that are never
 // multiplied (ring_last).
-template <bool KC, bool TAIL>
-__device__ __forceinline__ void ring_fill(const float *__restrict__ X, size_t r0, size_t k0, size_t ld, size_t rlast,
-                                          size_t klast, float *stage) {
-    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        if constexpr (KC) {
-            const int rb = w * 32 + s * 8, row = rb + (lane >> 3), p = lane & 7;
-            const size_t gr = r0 + row < rlast ? r0 + row : rlast, gk = k0 + 4 * (p ^ rk_c(row));
-            lds_load16(X + gr * ld + (!TAIL || gk < klast ? gk : klast), stage + rb * kRBK);
-        } else {
-            const int kb = w * 8 + s * 2, kr = kb + (lane >> 5), p = lane & 31;
-            const size_t gc = r0 + 4 * (p ^ rk_m(kr)), gk = k0 + kr;
-            lds_load16(X + (!TAIL || gk < klast ? gk : klast) * ld + (gc < rlast ? gc : rlast), stage + kb * BM);
-        }
-    }
-}
-
-// ring_fill for a stage with no k clamp, as base + per-lane offset: the
-// stage's base is X + r0 ld + k0 (k-contiguous) or X + k0 ld + r0, uniform
-// across the workgroup, and lane offsets (ring_offsets) stay fixed for the
-// whole K loop.  Same addresses, same LDS layout as ring_fill.
 struct RingOffs {
     unsigned o[4];
 };
 template <bool KC>
-__device__ __forceinline__ RingOffs ring_offsets(size_t r0, size_t ld, size_t rlast) {
+__device__ __forceinline__ RingOffs ring_offsets(size_t r0, size_t ld, size_t rlast, int kv) {
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
     RingOffs f;
 #pragma unroll
@@ -789,11 +772,13 @@ __device__ __forceinline__ RingOffs ring_offsets(size_t r0, size_t ld, size_t rl
         if constexpr (KC) {
             const int row = w * 32 + s * 8 + (lane >> 3), p = lane & 7;
             const size_t gr = r0 + row < rlast ? r0 + row : rlast;
-            f.o[s] = static_cast<unsigned>(((gr - r0) * ld + 4 * (p ^ rk_c(row))) * sizeof(float));
+            const int kk = 4 * (p ^ rk_c(row));
+            f.o[s] = static_cast<unsigned>(((gr - r0) * ld + (kk < kv - 4 ? kk : kv - 4)) * sizeof(float));
         } else {
             const int kr = w * 8 + s * 2 + (lane >> 5), p = lane & 31;
             const size_t gc = r0 + 4 * (p ^ rk_m(kr));
-            f.o[s] = static_cast<unsigned>((kr * ld + ((gc < rlast ? gc : rlast) - r0)) * sizeof(float));
+            f.o[s] = static_cast<unsigned>(((kr < kv - 1 ? kr : kv - 1) * ld + ((gc < rlast ? gc : rlast) - r0)) *
+                                           sizeof(float));
         }
     }
     return f;
@@ -809,22 +794,24 @@ __device__ __forceinline__ void ring_fill_at(const float *__restrict__ X, size_t
     for (int s = 0; s < 4; ++s) lds_load16_at(base, f.o[s], l0 + s * kWave * 16);
 }
 
-// Fills stage `st` (A at +0, B at +kRST) with the 32 k from kf: through
-// the offsets when the stage lies inside K (always without TAIL), else
-// with ring_fill's k clamp (ka, kb: the last k group or row of A and B).
+// A workgroup's fill offsets: whole stages (a, b) and, with TAIL, the last
+// tile of the split (at, bt; equal to a, b when it is whole).
+struct RingLanes {
+    RingOffs a, b, at, bt;
+};
+
+// Fills stage `st` (A at +0, B at +kRST) with the 32 k from kf; kl is the
+// k of the split's last tile, the only one that may be partial.
 template <bool KCA, bool KCB, bool TAIL>
 __device__ __forceinline__ void ring_fill_any(const float *__restrict__ A, const float *__restrict__ B, size_t lda,
-                                              size_t ldb, size_t m0, size_t n0, size_t ra, size_t rb, size_t ka,
-                                              size_t kb, size_t kf, const RingOffs &oa, const RingOffs &ob,
-                                              float *st) {
-    // the stage's last k, kf + 31, inside K: for A [M,K] ka = K - 4 (the
-    // last 4-k group's start), for A [K,M] ka = K - 1
-    if (!TAIL || kf + kRBK - (KCA ? 4 : 1) <= ka) {
-        ring_fill_at<KCA>(A, m0, kf, lda, oa, st);
-        ring_fill_at<KCB>(B, n0, kf, ldb, ob, st + kRST);
+                                              size_t ldb, size_t m0, size_t n0, size_t kf, size_t kl,
+                                              const RingLanes &L, float *st) {
+    if (!TAIL || kf != kl) {
+        ring_fill_at<KCA>(A, m0, kf, lda, L.a, st);
+        ring_fill_at<KCB>(B, n0, kf, ldb, L.b, st + kRST);
     } else {
-        ring_fill<KCA, TAIL>(A, m0, kf, lda, ra, ka, st);
-        ring_fill<KCB, TAIL>(B, n0, kf, ldb, rb, kb, st + kRST);
+        ring_fill_at<KCA>(A, m0, kf, lda, L.at, st);
+        ring_fill_at<KCB>(B, n0, kf, ldb, L.bt, st + kRST);
     }
 }
 
@@ -878,10 +865,9 @@ __device__ __forceinline__ void ring_block(const RingFrag &f, floatx16 (&acc)[2]
 // holds block 0 of cur on entry and block 0 of nxt on return.
 template <bool KCA, bool KCB, bool TAIL>
 __device__ __forceinline__ void ring_step(const float *__restrict__ A, const float *__restrict__ B, size_t lda,
-                                          size_t ldb, size_t m0, size_t n0, size_t ra, size_t rb, size_t ka,
-                                          size_t kb, size_t kf, float *cur, const float *nxt, RingFrag &f0,
-                                          floatx16 (&acc)[2][2], int wm, int wn, int l32, int lhi,
-                                          const RingOffs &oa, const RingOffs &ob) {
+                                          size_t ldb, size_t m0, size_t n0, size_t kf, size_t kl, float *cur,
+                                          const float *nxt, RingFrag &f0, floatx16 (&acc)[2][2], int wm, int wn,
+                                          int l32, int lhi, const RingLanes &L) {
     RingFrag f1, f2;
     ring_frags<KCA, KCB>(cur, 1, wm, wn, l32, lhi, f1);
     ring_block<KCA, KCB>(f0, acc);
@@ -891,7 +877,7 @@ __device__ __forceinline__ void ring_step(const float *__restrict__ A, const flo
     ring_block<KCA, KCB>(f2, acc);
     ring_barrier<2 * kRPS>();  // tile t+1 landed; every wave done reading cur
     ring_frags<KCA, KCB>(nxt, 0, wm, wn, l32, lhi, f0);
-    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kf, oa, ob, cur);
+    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, kf, kl, L, cur);
     ring_block<KCA, KCB>(f1, acc);
 }
 
@@ -929,8 +915,7 @@ __device__ __forceinline__ void ring_gemm(const float *__restrict__ A, const flo
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int wm = wave >> 1, wn = wave & 1, l32 = lane & 31, lhi = lane >> 5;
     const size_t lda = KCA ? K : M, ldb = KCB ? K : N;
-    const size_t ra = KCA ? M - 1 : M - 4, rb = KCB ? N - 1 : N - 4;  // ring_fill's clamps
-    const size_t ka = KCA ? K - 4 : K - 1, kb = KCB ? K - 4 : K - 1;
+    const size_t ra = KCA ? M - 1 : M - 4, rb = KCB ? N - 1 : N - 4;  // ring_offsets' row clamps
 
     floatx16 acc[2][2];
 #pragma unroll
@@ -945,17 +930,24 @@ __device__ __forceinline__ void ring_gemm(const float *__restrict__ A, const flo
     // into stages whose fragments go unused.
     const size_t len = kend - kbeg, T = (len + kRBK - 1) / kRBK;
     auto kt = [&](size_t t) { return kbeg + (t < T ? t : T - 1) * kRBK; };
-    const RingOffs oa = ring_offsets<KCA>(m0, lda, ra), ob = ring_offsets<KCB>(n0, ldb, rb);
-    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kt(0), oa, ob, s0);
-    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kt(1), oa, ob, s1);
-    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kt(2), oa, ob, s2);
-    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kt(3), oa, ob, s3);
+    const size_t kl = kt(T - 1);
+    RingLanes L;
+    L.a = ring_offsets<KCA>(m0, lda, ra, kRBK);
+    L.b = ring_offsets<KCB>(n0, ldb, rb, kRBK);
+    if constexpr (TAIL) {
+        const int kv = static_cast<int>(len - (T - 1) * kRBK);  // 8..32
+        L.at = ring_offsets<KCA>(m0, lda, ra, kv);
+        L.bt = ring_offsets<KCB>(n0, ldb, rb, kv);
+    }
+    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, kt(0), kl, L, s0);
+    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, kt(1), kl, L, s1);
+    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, kt(2), kl, L, s2);
+    ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, kt(3), kl, L, s3);
     ring_barrier<3 * kRPS>();
     RingFrag f0;
     ring_frags<KCA, KCB>(s0, 0, wm, wn, l32, lhi, f0);
 #define CXM_RING_STEP(T4, CUR, NXT) \
-    ring_step<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, ra, rb, ka, kb, kt(T4), CUR, NXT, f0, acc, wm, wn, l32, lhi, \
-                              oa, ob)
+    ring_step<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, kt(T4), kl, CUR, NXT, f0, acc, wm, wn, l32, lhi, L)
     if constexpr (!TAIL) {
         for (size_t t = 0; t < T; t += 4) {  // T is a multiple of 4
             CXM_RING_STEP(t + 4, s0, s1);
