@@ -188,9 +188,16 @@ __device__ __forceinline__ void lds_load16(const void *gsrc, const void *lds) {
 // The same load from a wave-uniform base (an SGPR pair) plus a 32-bit
 // per-lane byte offset (the saddr form): the lane's address costs no 64-bit
 // vector arithmetic.
-// `lds` is the LDS byte address (lds_addr), wave-uniform.
+// `base` and `lds` (the LDS byte address, lds_addr) are the same in every
+// lane; read from the first lane, they are scalar values for the
+// instruction's SGPR operands whatever registers the compiler held them in.
 __device__ __forceinline__ void lds_load16_at(const void *base, unsigned off, unsigned lds) {
-    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+    const size_t b = reinterpret_cast<size_t>(base);
+    const unsigned lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(b));
+    const unsigned hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(b >> 32));
+    const void *sb = reinterpret_cast<const void *>((static_cast<size_t>(hi) << 32) | lo);
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(sb), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
 }
 // LDS byte address of a __shared__ location, as a wave-uniform value.
 __device__ __forceinline__ unsigned lds_addr(const void *p) {
