@@ -26,7 +26,7 @@ def gpu_reduce(op, x, sizes, ptr_offset_floats=0):
     buf = np.concatenate([np.zeros(ptr_offset_floats, np.float32), flat])
     dx = DeviceArray.from_numpy(buf)
     n_out = 1 if len(sizes) == 1 else sizes[0] * sizes[2]
-    dz = DeviceArray((n_out,), np.int32 if op == "argmax" else np.float32)
+    dz = DeviceArray((n_out,), np.int32 if op in ("argmax", "argmin") else np.float32)
     xp = dx.ptr + 4 * ptr_offset_floats
     if len(sizes) == 1:
         call(f"cxm_reduce_{op}_flat_f32", xp, dz.ptr, sizes[0], None)
@@ -46,7 +46,7 @@ def abs_sums(x, sizes):
 def check(op, x, sizes, orc, **kw):
     got = gpu_reduce(op, x, sizes, **kw)
     ref = orc.reduce_flat(op, x) if len(sizes) == 1 else orc.reduce_axis(op, x, *sizes)
-    if op in ("max", "argmax"):
+    if op in ("max", "argmax", "min", "argmin"):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (op, sizes)
     else:
         tol = SUM_TOL * abs_sums(x, sizes)
@@ -260,3 +260,4 @@ def test_unaligned_ragged_rows(hip, orc, off, sizes, op):
     its first segment, the body still takes 128-bit loads."""
     x = SplitMix64(off * 7919 + sum(sizes)).normal(sizes if len(sizes) > 1 else sizes[0], 0.0, 2.0)
     check(op, x, sizes, orc, ptr_offset_floats=off)
+
