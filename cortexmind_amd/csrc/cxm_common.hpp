@@ -109,7 +109,11 @@ struct GemmSpec {
     int ta, tb;
     Epilogue epi;
 };
-int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st);
+// With `side`, the launch also runs the MLP step's side work (mlp_side.hpp)
+// on the CUs the products leave free when there are at least 8 of them;
+// side->wgs says how many workgroups took it (0: none, the caller runs it).
+struct StepSide;
+int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st, StepSide *side = nullptr);
 // b[j] = b[j] - lr * sum_i x[i, j] over x [rows, cols]: a bias gradient
 // (reduce::sum over axis 0) and its SGD step in one pass (reduce.hip).
 int colsum_sgd(const float *x, float *b, size_t rows, size_t cols, float lr, cxm_stream_t s);

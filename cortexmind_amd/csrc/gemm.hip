@@ -23,6 +23,7 @@
 #include <atomic>
 
 #include "cxm_common.hpp"
+#include "mlp_side.hpp"
 
 namespace cxm {
 namespace {
@@ -1015,7 +1016,12 @@ struct RingArgs {
     unsigned wgs;  // workgroups of this product (a multiple of 8 for the XCD order, else dispatch order)
 };
 template <bool KCA, bool KCB>
-__global__ __launch_bounds__(kRingThreads) void k_gemm_ring_pair(RingArgs g0, RingArgs g1) {
+__global__ __launch_bounds__(kRingThreads) void k_gemm_ring_pair(RingArgs g0, RingArgs g1, StepSide side) {
+    if (blockIdx.x >= g0.wgs + g1.wgs) {  // dispatched after every product workgroup: the free CUs
+        __shared__ float slds[16][64];
+        step_side(side, blockIdx.x - g0.wgs - g1.wgs, slds);
+        return;
+    }
     const bool second = blockIdx.x >= g0.wgs;
     const RingArgs &g = second ? g1 : g0;
     const unsigned b = second ? blockIdx.x - g0.wgs : blockIdx.x;
@@ -1468,8 +1474,10 @@ constexpr size_t kRingCUs = 256;
 
 }  // namespace
 
-int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st) {
+int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st, StepSide *side) {
     size_t ta_t, ta_n, ta_s, ta_k, tb_t, tb_n, tb_s, tb_k;
+    StepSide none{};
+    if (side) side->wgs = 0;
     if (!a.A || !a.B || !a.C || !b.A || !b.B || !b.C || a.ta != b.ta || a.tb != b.tb) return 1;
     if (a.epi.act != CXM_ACT_NONE && a.epi.act != CXM_ACT_RELU) return 1;
     if (b.epi.act != CXM_ACT_NONE && b.epi.act != CXM_ACT_RELU) return 1;
@@ -1499,12 +1507,19 @@ int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st) {
     const RingArgs gb{b.A, b.B, b.C, b.M, b.N, b.K, static_cast<unsigned>(tb_n), static_cast<unsigned>(tb_s), tb_k,
                       b.epi, part ? part + pa : nullptr, counters ? ctr(counters, ta_t) : nullptr,
                       static_cast<unsigned>(wb)};
+    // side work only on CUs the products leave free (one ring workgroup
+    // fills a CU's LDS), so that it never delays them
+    const size_t nside = side && wa + wb + 8 <= kRingCUs ? kRingCUs - (wa + wb) : 0;
+    StepSide &sd = nside ? *side : none;
+    sd.wgs = static_cast<unsigned>(nside);
     hipStream_t s = reinterpret_cast<hipStream_t>(st);
-    const dim3 grid(static_cast<unsigned>(wa + wb));
-    if (!a.ta && !a.tb) hipLaunchKernelGGL((k_gemm_ring_pair<true, false>), grid, dim3(kRingThreads), 0, s, ga, gb);
-    else if (a.ta && !a.tb) hipLaunchKernelGGL((k_gemm_ring_pair<false, false>), grid, dim3(kRingThreads), 0, s, ga, gb);
-    else hipLaunchKernelGGL((k_gemm_ring_pair<true, true>), grid, dim3(kRingThreads), 0, s, ga, gb);
-    return launch_status();
+    const dim3 grid(static_cast<unsigned>(wa + wb + nside));
+    if (!a.ta && !a.tb) hipLaunchKernelGGL((k_gemm_ring_pair<true, false>), grid, dim3(kRingThreads), 0, s, ga, gb, sd);
+    else if (a.ta && !a.tb) hipLaunchKernelGGL((k_gemm_ring_pair<false, false>), grid, dim3(kRingThreads), 0, s, ga, gb, sd);
+    else hipLaunchKernelGGL((k_gemm_ring_pair<true, true>), grid, dim3(kRingThreads), 0, s, ga, gb, sd);
+    const int rc = launch_status();
+    if (rc && side) side->wgs = 0;
+    return rc;
 }
 
 }  // namespace cxm

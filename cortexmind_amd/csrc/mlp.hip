@@ -33,6 +33,7 @@
 #include <new>
 
 #include "cxm_common.hpp"
+#include "mlp_side.hpp"
 
 struct cxm_mlp3 {
     size_t b, d0, d1, d2, d3;
@@ -49,9 +50,9 @@ namespace {
 constexpr int kHeadThreads = 1024;
 constexpr int kHeadRows = 16;  // rows per workgroup: the 16 of a 16x16 MFMA tile
 constexpr int kHeadMaxD2 = 1024;
-// partial columns after the d2 of gb2: the loss, then gb3[0..d3-1] (up to
-// 17 values; 32 keeps the gW3 columns that follow 16-byte aligned)
-constexpr int kHeadExtra = 32;
+// partial columns after the d2 of gb2 (kHeadExtra, mlp_side.hpp): the loss,
+// then gb3[0..d3-1] (up to 17 values; 32 keeps the gW3 columns that follow
+// 16-byte aligned)
 // A head workgroup's partial row: gb2 [D2], the loss and gb3 [kHeadExtra], gW3 [D3][D2].
 __host__ __device__ inline size_t head_part_width(size_t d2, size_t d3) { return d2 + kHeadExtra + d3 * d2; }
 
@@ -326,13 +327,14 @@ __global__ __launch_bounds__(kFinishThreads) void k_head_finish(const float *__r
 }
 
 
-int run_head(const cxm_mlp3 *h, const int32_t *labels, float *w3, float *b3, float *b2, float lr, float *loss,
-             hipStream_t s) {
+int run_head(const cxm_mlp3 *h, const int32_t *labels, const float *w3, const float *b3, hipStream_t s) {
     const float inv_b = 1.0f / static_cast<float>(h->b);
     hipLaunchKernelGGL(k_mlp_head, dim3(h->head_blocks), dim3(kHeadThreads), 0, s, h->h2, w3, b3, labels,
                        h->dh2, h->b, h->d2, h->d3, inv_b, h->part);
-    int rc = launch_status();
-    if (rc) return rc;
+    return launch_status();
+}
+
+int run_head_finish(const cxm_mlp3 *h, float *w3, float *b3, float *b2, float lr, float *loss, hipStream_t s) {
     const size_t pw = head_part_width(h->d2, h->d3);
     hipLaunchKernelGGL(k_head_finish, dim3(ceil_div(pw, kFinishCols)), dim3(kFinishThreads), 0, s, h->part,
                        h->head_blocks, h->d2, h->d3, h->b, lr, loss, b2, b3, w3);
@@ -403,8 +405,9 @@ int cxm_mlp3_step_f32(cxm_mlp3 *h, const float *x, const int32_t *labels, float 
     CXM_TRY(cxm::gemm_ex(x, w1, h->h1, B, d0, d1, 0, 0, Epilogue{b1, nullptr, CXM_ACT_RELU, 0, 0.0f}, s));
     CXM_TRY(cxm::gemm_ex(h->h1, w2, h->h2, B, d1, d2, 0, 0, Epilogue{b2, nullptr, CXM_ACT_RELU, 0, 0.0f}, s));
     if (h->fused_head) {
-        // output layer fused: logits, loss, dl, dh2 (reads W3), then the loss, b3, b2 and W3 updates
-        CXM_TRY(cxm::run_head(h, labels, w3, b3, b2, lr, loss, reinterpret_cast<hipStream_t>(s)));
+        // output layer fused: logits, loss, dl, dh2 (reads W3); the loss, b3,
+        // b2 and W3 updates follow with the weight gradients (below)
+        CXM_TRY(cxm::run_head(h, labels, w3, b3, reinterpret_cast<hipStream_t>(s)));
     } else {
         CXM_TRY(cxm::gemm_ex(h->h2, w3, h->lg, B, d2, d3, 0, 0, Epilogue{b3, nullptr, CXM_ACT_NONE, 0, 0.0f}, s));
         CXM_TRY(cxm_softmax_xent_f32(h->lg, labels, loss, h->dl, B, d3, s));
@@ -419,10 +422,32 @@ int cxm_mlp3_step_f32(cxm_mlp3 *h, const float *x, const int32_t *labels, float 
     // the two weight gradients with their SGD steps, W2 -= lr h1^T dH2 and
     // W1 -= lr x^T dH1: independent, so one launch where both take the ring
     // (the second's workgroups fill the CUs the first releases); else in turn
+    // (the output layer's finish and the layer-1 bias step ride along on the
+    // CUs the pair leaves free when there are enough; else they follow)
+    cxm::StepSide side{};
+    if (h->fused_head) {
+        side.part = h->part;
+        side.blocks = h->head_blocks;
+        side.pw = static_cast<unsigned>(cxm::head_part_width(d2, d3));
+        side.d2 = static_cast<unsigned>(d2);
+        side.d3 = static_cast<unsigned>(d3);
+        side.b = static_cast<unsigned>(B);
+        side.loss = loss;
+        side.b2 = b2;
+        side.b3 = b3;
+        side.w3 = w3;
+    }
+    side.lr = lr;
+    if (d1 % 4 == 0 && B <= 0xffffffffu && d1 <= 0xffffffffu) {
+        side.dh1 = h->dh1;
+        side.b1 = b1;
+        side.d1 = static_cast<unsigned>(d1);
+        side.b = static_cast<unsigned>(B);
+    }
     {
         const cxm::GemmSpec g2{h->h1, h->dh2, w2, d1, B, d2, 1, 0, sgd};
         const cxm::GemmSpec g1{x, h->dh1, w1, d0, B, d1, 1, 0, sgd};
-        rc = cxm::gemm_ex_pair(g2, g1, s);
+        rc = cxm::gemm_ex_pair(g2, g1, s, &side);
         if (rc == 1) {
             CXM_TRY(cxm::gemm_ex(h->h1, h->dh2, w2, d1, B, d2, 1, 0, sgd, s));
             CXM_TRY(cxm::gemm_ex(x, h->dh1, w1, d0, B, d1, 1, 0, sgd, s));
@@ -430,8 +455,11 @@ int cxm_mlp3_step_f32(cxm_mlp3 *h, const float *x, const int32_t *labels, float 
             return rc;
         }
     }
+    if (side.wgs == 0 || !side.part) {
+        if (h->fused_head) CXM_TRY(cxm::run_head_finish(h, w3, b3, b2, lr, loss, reinterpret_cast<hipStream_t>(s)));
+    }
     // layer 1 bias
-    CXM_TRY(cxm::colsum_sgd(h->dh1, b1, B, d1, lr, s));
+    if (side.wgs == 0 || !side.dh1) CXM_TRY(cxm::colsum_sgd(h->dh1, b1, B, d1, lr, s));
 #undef CXM_TRY
     return CXM_OK;
 }
