@@ -628,7 +628,11 @@ def main():
     if not args.no_extra:
         wl = {}
         for name in [w for w in ["c1", "c3", "c4", "c5", "more", "g16"] if w != args.workload]:
-            r = run_workload(name, max(20, args.steps // 2), 2, E, D, Event, sync)
+            # Untimed warm-up of each extra workload: the MLP step runs its
+            # first ~100 steps (~35 ms) up to 13% slower on a box that has
+            # just run bandwidth work (5 steps: 0.398 ms, 25: 0.370, 100 and
+            # after: 0.351), so it gets 100; the others 10.
+            r = run_workload(name, max(20, args.steps // 2), 100 if name == "c5" else 10, E, D, Event, sync)
             wl[name] = {"workload": r["config"]["workload"], "value": round(r["value"], 2),
                         "unit": r["unit"], "ms_per_step": round(r["ms_per_step"], 5),
                         "roofline": r["roofline"], "per_op": r["per_op"]}
