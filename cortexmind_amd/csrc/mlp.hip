@@ -425,7 +425,8 @@ int cxm_mlp3_step_f32(cxm_mlp3 *h, const float *x, const int32_t *labels, float 
     // (the output layer's finish and the layer-1 bias step ride along on the
     // CUs the pair leaves free when there are enough; else they follow)
     cxm::StepSide side{};
-    if (h->fused_head) {
+    const bool side_ok = B <= 0xffffffffu && d1 <= 0xffffffffu;  // its sizes are 32-bit
+    if (h->fused_head && side_ok) {
         side.part = h->part;
         side.blocks = h->head_blocks;
         side.pw = static_cast<unsigned>(cxm::head_part_width(d2, d3));
@@ -438,7 +439,7 @@ int cxm_mlp3_step_f32(cxm_mlp3 *h, const float *x, const int32_t *labels, float 
         side.w3 = w3;
     }
     side.lr = lr;
-    if (d1 % 4 == 0 && B <= 0xffffffffu && d1 <= 0xffffffffu) {
+    if (d1 % 4 == 0 && side_ok) {
         side.dh1 = h->dh1;
         side.b1 = b1;
         side.d1 = static_cast<unsigned>(d1);
