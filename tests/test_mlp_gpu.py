@@ -111,3 +111,26 @@ def test_mlp_shapes_vs_oracle(hip, orc, batch, dims):
         w = "w" + k[1]
         scale = max(np.abs(params[w]).max(), np.abs(ref[w]).max())
         assert np.max(np.abs(final[k] - ref[k])) <= 1e-4 * scale, k
+
+
+def test_mlp_pair_without_free_cus_vs_oracle(hip, orc):
+    """Hidden widths of 2048: the two weight gradients (256 + 112 ring tiles)
+    fill the chip, so the paired launch has no free CUs for the output
+    layer's finish and the layer-1 bias step, which then run as their own
+    kernels (at the C5 shape they ride on the pair's 16 free CUs).  Three
+    steps at the C5 rate (lr 0.01: at 0.05 this width diverges and the
+    loss amplifies rounding differences past the bar by the third step)
+    against the oracle, same bars as above."""
+    x, labels, params = c5_mlp(batch=128, dims=(784, 2048, 2048, 10))
+    g = SplitMix64(2048)
+    for k in ("b1", "b2", "b3"):
+        params[k] = g.normal(params[k].shape, 0.0, 0.1)
+    losses, final = gpu_steps(x, labels, params, 0.01, 3)
+    ref = {k: v.copy() for k, v in params.items()}
+    ref_losses = [orc.mlp_step(x, labels, ref, 0.01) for _ in range(3)]
+    for got, want in zip(losses, ref_losses):
+        assert abs(got - want) <= 1e-5 * max(abs(want), 1e-3), (losses, ref_losses)
+    for k in ref:
+        w = "w" + k[1]
+        scale = max(np.abs(params[w]).max(), np.abs(ref[w]).max())
+        assert np.max(np.abs(final[k] - ref[k])) <= 1e-4 * scale, k
