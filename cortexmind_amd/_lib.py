@@ -20,6 +20,7 @@ OK = 0
 E_INVALID = -1
 E_TOO_LARGE = -2
 E_NO_DEVICE = -3
+E_CAPTURE = -4
 
 OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_MAX, OP_MIN, OP_POW = range(7)
 DT_F32, DT_BF16, DT_F16 = range(3)
@@ -60,6 +61,7 @@ SIGNATURES = {
     "cxm_event_elapsed_ms": [ctypes.POINTER(_F), _P, _P],
     "cxm_event_destroy": [_P],
     "cxm_release_workspaces": [],
+    "cxm_workspace_query": [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_SZ), ctypes.POINTER(_I)],
     "cxm_act_bwd_f32": [_P, _P, _P, _SZ, _I, _P],
     "cxm_convert": [_P, _I, _P, _I, _SZ, _P],
     "cxm_binary_t": [_P, _P, _P, _SZ, _I, _I, _P],
@@ -116,6 +118,7 @@ SIGNATURES = {
     "cxm_softmax_xent_f32": [_P, _P, _P, _P, _SZ, _SZ, _P],
     "cxm_sgd_f32": [_P, _P, _F, _SZ, _P],
     "cxm_reduce_sum_bwd_f32": [_P, _P, _SZ, _SZ, _SZ, _I, _P],
+    "cxm_mlp3_last_side": [_P, ctypes.POINTER(ctypes.c_uint)],
     "cxm_mlp3_create": [ctypes.POINTER(_P), _SZ, _SZ, _SZ, _SZ, _SZ],
     "cxm_mlp3_step_f32": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P],
     "cxm_mlp3_destroy": [_P],

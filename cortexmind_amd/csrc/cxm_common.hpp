@@ -61,14 +61,18 @@ int get_exchange(cxm_stream_t s, size_t rows, Exchange *x);
 // Tagged partial slots of the flat reductions, one region per (device,
 // stream), kept apart from the workspace scratch.  Slot i is a 64-bit word
 // (32-bit partial | tag << 32).  Each call takes a new tag (`epoch`, never
-// 0, from a host counter per region): its writers store their partials
-// with it and its reader waits for it, so a slot an earlier call left, of
-// any shape, never carries the current tag; calls on one stream are
-// ordered, so a write of an earlier call has landed before a later call
-// starts.  A graph replays its launches with the tags they were captured
-// with, so a call made under stream capture (`clear`) also has its reader
-// put every slot it consumed back to tag 0.  Zero-filled when allocated;
-// grows on demand (after a stream sync).
+// 0, from next_tag()): its writers store their partials with it and its
+// reader waits for it, so a slot an earlier call left, of any shape, on any
+// stream, never carries the current tag; calls on one stream are ordered,
+// so a write of an earlier call has landed before a later call starts.  A
+// graph replays its launches with the tags they were captured with, so a
+// call made under stream capture (`clear`) also has its reader put every
+// slot it consumed back to tag 0.  Zero-filled when allocated; grows on
+// demand (after a stream sync).  Under capture, a region that is missing or
+// too small is CXM_E_CAPTURE (nothing is allocated, filled or waited for);
+// one handed to a captured launch stays allocated until the stream is
+// destroyed or cxm_release_workspaces runs.  get_workspace and
+// get_exchange follow the same rules.
 struct TaggedSlots {
     unsigned long long *slots;
     size_t n;
@@ -76,6 +80,28 @@ struct TaggedSlots {
     int clear;
 };
 int get_tagged(cxm_stream_t s, size_t n, TaggedSlots *t);
+
+// A new tag for the tagged slots, from one counter for the whole process
+// (never 0, the empty slot's tag).
+unsigned next_tag();
+
+// Compute units and XCDs (each with its own L2) of the current device,
+// read once per device.  Workgroups of a dispatch go to the XCDs round
+// robin by linear workgroup id.
+struct DevLayout {
+    int cus;
+    int xccs;
+};
+int device_layout(DevLayout *out);
+// The current device's compute units (256 when the query fails).
+inline size_t device_cus() {
+    DevLayout l{0, 1};
+    return device_layout(&l) == CXM_OK && l.cus > 0 ? static_cast<size_t>(l.cus) : 256;
+}
+
+// The current device's region `which` (0 workspace, 1 exchange, 2 tagged
+// slots) of stream s: base, size and whether a captured launch holds it.
+int workspace_query(cxm_stream_t s, int which, void **base, size_t *bytes, int *pinned);
 
 // Polls a waiting workgroup makes for a peer's partial before it computes
 // that partial itself (cxm_exchange_wait_limit).
@@ -249,26 +275,39 @@ struct SqSumOp : SumOp {
     __device__ static T accum(T a, float v, int) { return fmaf(v, v, a); }
 };
 
+// max / min of the reductions (and the softmax's row max): IEEE 754-2019
+// maximum / minimum, one v_maximum3_f32 / v_minimum3_f32 on gfx950: NaN
+// when either operand is NaN, and +0 above -0.  Both are associative and
+// commutative on every input, NaN and signed zeros included, so any tree
+// gives the same bits.  The reference folds _mm256_max_ps lane by lane
+// (Engine/AVX2/functions.hpp:314-316: the second operand on NaN and on
+// ties), whose result with a NaN or a +0/-0 tie depends on where they sit;
+// without them the two agree bit for bit.  The flat and row forms start
+// from -FLT_MAX (max) / FLT_MAX (min) as the reference does.
 struct MaxOp {
     using T = float;
     static constexpr bool kShift = false;
     __device__ static T identity() { return -FLT_MAX; }
-    __device__ static T combine(T a, T b) { return vmax(a, b); }
-    __device__ static T accum(T a, float v, int) { return vmax(a, v); }
+    __device__ static T combine(T a, T b) { return __builtin_elementwise_maximum(a, b); }
+    __device__ static T accum(T a, float v, int) { return __builtin_elementwise_maximum(a, v); }
 };
 
-// min as _mm256_min_ps(a, b): a when a < b, else b; flat and row forms start
-// from FLT_MAX.
 struct MinOp {
     using T = float;
     static constexpr bool kShift = false;
     __device__ static T identity() { return FLT_MAX; }
-    __device__ static T combine(T a, T b) { return a < b ? a : b; }
-    __device__ static T accum(T a, float v, int) { return a < v ? a : v; }
+    __device__ static T combine(T a, T b) { return __builtin_elementwise_minimum(a, b); }
+    __device__ static T accum(T a, float v, int) { return __builtin_elementwise_minimum(a, v); }
 };
 
-// Lexicographic (value, index): larger value wins; equal values keep the
-// smaller index, i.e. the first maximum in storage order.
+// Lexicographic (value, index): larger value wins; equal values (+0 and -0
+// among them) keep the smaller index, i.e. the first maximum in storage
+// order.  A NaN element never wins a comparison, so NaNs are skipped --
+// except the first element of the row, column or flat array: the reference
+// starts from it and takes only strictly greater values after it
+// (reduce.cpp:442-455, 483-521), so a NaN there stays the answer.  The
+// kernels fold that case in by replacing the first element's pair with
+// first_nan(), which beats every pair, and write its index -1 as 0.
 struct ArgPair {
     float v;
     int i;
@@ -277,6 +316,7 @@ struct ArgMaxOp {
     using T = ArgPair;
     static constexpr bool kShift = false;
     __device__ static T identity() { return {-INFINITY, 0x7fffffff}; }
+    __device__ static T first_nan() { return {INFINITY, -1}; }
     __device__ static T combine(T a, T b) {
         const bool take_b = (b.v > a.v) || (b.v == a.v && b.i < a.i);
         return take_b ? b : a;
@@ -288,12 +328,20 @@ struct ArgMinOp {
     using T = ArgPair;
     static constexpr bool kShift = false;
     __device__ static T identity() { return {INFINITY, 0x7fffffff}; }
+    __device__ static T first_nan() { return {-INFINITY, -1}; }
     __device__ static T combine(T a, T b) {
         const bool take_b = (b.v < a.v) || (b.v == a.v && b.i < a.i);
         return take_b ? b : a;
     }
     __device__ static T accum(T a, float v, int i) { return combine(a, T{v, i}); }
 };
+// argmax / argmin: the pair of a NaN first element (x0) wins outright.
+template <class Op>
+__device__ __forceinline__ void first_nan_fix(typename Op::T &a, float x0) {
+    if constexpr (__is_same(typename Op::T, ArgPair)) {
+        if (__builtin_isnan(x0)) a = Op::first_nan();
+    }
+}
 
 template <int CTRL>
 __device__ __forceinline__ ArgPair dpp(ArgPair p) {

@@ -1384,13 +1384,14 @@ int gemm_ex(const float *A, const float *B, float *C, size_t M, size_t K, size_t
     }
     const size_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const size_t tiles = tiles_m * tiles_n;
-    // Split K when the tile grid alone cannot fill the chip's 256 CUs;
+    // Split K when the tile grid alone cannot fill the chip's CUs (256 here);
     // each split keeps at least 256 of K.
     size_t splits = 1;
-    // (at most 256 workgroups: one 8-wave workgroup fills a CU, and a 257th
-    // would run as a second round)
-    if (tiles < 192 && K >= 512) {
-        splits = 256 / tiles;
+    // (at most one workgroup per CU: one 8-wave workgroup fills a CU, and
+    // one more would run as a second round)
+    const size_t cus = device_cus();
+    if (tiles < cus * 3 / 4 && K >= 512) {
+        splits = cus / tiles;
         const size_t max_splits = K / 256;
         if (splits > max_splits) splits = max_splits;
         if (splits < 1) splits = 1;
@@ -1440,8 +1441,9 @@ bool ring_plan(const float *A, const float *B, size_t M, size_t K, size_t N, int
     const bool ring_ok = ring_shape_ok(A, B, M, K, N, ta, tb);
     const size_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN, t = tm * tn;
     size_t sp = 1;
-    if (t < 192 && K >= 512) {
-        sp = 256 / t;
+    const size_t cus = device_cus();
+    if (t < cus * 3 / 4 && K >= 512) {
+        sp = cus / t;
         const size_t max_splits = K / 256;
         if (sp > max_splits) sp = max_splits;
         if (sp < 1) sp = 1;
@@ -1469,9 +1471,6 @@ bool ring_resplit(size_t K, size_t sp, size_t *splits, size_t *kper) {
     return true;
 }
 
-// CUs of the part: one ring workgroup (128 KiB of LDS) per CU.
-constexpr size_t kRingCUs = 256;
-
 }  // namespace
 
 int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st, StepSide *side) {
@@ -1485,9 +1484,11 @@ int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st, StepSide
     if (!ring_plan(b.A, b.B, b.M, b.K, b.N, b.ta, b.tb, &tb_t, &tb_n, &tb_s, &tb_k)) return 1;
     // Each plan alone fills the chip; together they would run as two rounds
     // of workgroups, each paying the ring's fill and epilogue.  One split
-    // count for both that keeps the pair within one round instead.
-    if (ta_t * ta_s + tb_t * tb_s > kRingCUs) {
-        const size_t sp = std::max<size_t>(1, kRingCUs / (ta_t + tb_t));
+    // count for both that keeps the pair within one round instead (one ring
+    // workgroup, 128 KiB of LDS, per CU).
+    const size_t cus = device_cus();
+    if (ta_t * ta_s + tb_t * tb_s > cus) {
+        const size_t sp = std::max<size_t>(1, cus / (ta_t + tb_t));
         if (!ring_resplit(a.K, sp, &ta_s, &ta_k) || !ring_resplit(b.K, sp, &tb_s, &tb_k)) return 1;
     }
     const size_t wa = ta_t * ta_s, wb = tb_t * tb_s;
@@ -1509,7 +1510,7 @@ int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st, StepSide
                       static_cast<unsigned>(wb)};
     // side work only on CUs the products leave free (one ring workgroup
     // fills a CU's LDS), so that it never delays them
-    const size_t nside = side && wa + wb + 8 <= kRingCUs ? kRingCUs - (wa + wb) : 0;
+    const size_t nside = side && wa + wb + 8 <= cus ? cus - (wa + wb) : 0;
     StepSide &sd = nside ? *side : none;
     sd.wgs = static_cast<unsigned>(nside);
     hipStream_t s = reinterpret_cast<hipStream_t>(st);

@@ -42,6 +42,7 @@ struct cxm_mlp3 {
     unsigned head_blocks;
     int fused_head;  // 1: the fused output layer (d3 <= 16, d2 <= 1024, d2 % 4 == 0); 0: unfused
     void *block;  // one allocation holding all of the above
+    unsigned last_side;  // side workgroups of the last step's paired launch (0: separate kernels)
 };
 
 namespace cxm {
@@ -445,6 +446,7 @@ int cxm_mlp3_step_f32(cxm_mlp3 *h, const float *x, const int32_t *labels, float 
         side.d1 = static_cast<unsigned>(d1);
         side.b = static_cast<unsigned>(B);
     }
+    h->last_side = 0;
     {
         const cxm::GemmSpec g2{h->h1, h->dh2, w2, d1, B, d2, 1, 0, sgd};
         const cxm::GemmSpec g1{x, h->dh1, w1, d0, B, d1, 1, 0, sgd};
@@ -461,7 +463,14 @@ int cxm_mlp3_step_f32(cxm_mlp3 *h, const float *x, const int32_t *labels, float 
     }
     // layer 1 bias
     if (side.wgs == 0 || !side.dh1) CXM_TRY(cxm::colsum_sgd(h->dh1, b1, B, d1, lr, s));
+    h->last_side = side.wgs;
 #undef CXM_TRY
+    return CXM_OK;
+}
+
+int cxm_mlp3_last_side(const cxm_mlp3 *h, unsigned *wgs) {
+    if (!h || !wgs) return CXM_E_INVALID;
+    *wgs = h->last_side;
     return CXM_OK;
 }
 

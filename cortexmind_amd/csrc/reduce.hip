@@ -50,7 +50,6 @@ __global__ void k_zero_words(unsigned *p, size_t n) {
 
 constexpr int kMaxDevices = 64;
 std::atomic<unsigned char *> g_fixed[kMaxDevices];
-std::atomic<unsigned> g_fixed_epoch[kMaxDevices];  // tag of the last call on each device's static slots
 std::mutex g_fixed_mu;
 
 // Device address of the current device's `scratch`, looked up once per
@@ -114,13 +113,9 @@ int acquire(bool fixed, cxm_stream_t s, size_t counters, size_t bytes, size_t ta
     sc->counters = reinterpret_cast<unsigned *>(base);
     sc->part = base + kFixedZeroBytes;
     if (tagged) {
-        int dev = 0;
-        const hipError_t e = hipGetDevice(&dev);
-        if (e != hipSuccess) return static_cast<int>(e);
-        unsigned ep = g_fixed_epoch[dev].fetch_add(1u, std::memory_order_relaxed) + 1u;
-        if (ep == 0) ep = g_fixed_epoch[dev].fetch_add(1u, std::memory_order_relaxed) + 1u;
         // the static slots serve any caller, captured or not: always cleared
-        sc->tagged = TaggedSlots{reinterpret_cast<unsigned long long *>(base + kFixedCounterBytes), kFixedTagged, ep, 1};
+        sc->tagged = TaggedSlots{reinterpret_cast<unsigned long long *>(base + kFixedCounterBytes), kFixedTagged,
+                                 next_tag(), 1};
     }
     return CXM_OK;
 }
@@ -151,7 +146,7 @@ struct OutDesc {
 template <class Op>
 __device__ __forceinline__ void write_out(const OutDesc &o, size_t q, typename Op::T r) {
     if constexpr (std::is_same_v<typename Op::T, ArgPair>) {
-        static_cast<int32_t *>(o.z)[q] = r.i;
+        static_cast<int32_t *>(o.z)[q] = r.i < 0 ? 0 : r.i;  // -1: a NaN first element
     } else if constexpr (std::is_same_v<typename Op::T, Pow2>) {
         // sum of squared deviations, rounded once to fp32, then scaled as
         // reduce.cpp scales it (population variance)
@@ -273,6 +268,7 @@ __device__ __forceinline__ typename Op::T row_segment(const float *__restrict__ 
             if constexpr (Op::kShift) e = e - k;
             acc[0] = Op::accum(acc[0], e, i);
         }
+        if (tid == 0) first_nan_fix<Op>(acc[0], xr[0]);
     }
     T r = Op::combine(Op::combine(acc[0], acc[1]), Op::combine(acc[2], acc[3]));
     return block_reduce<Op, kBlock>(r, lds);
@@ -307,6 +303,7 @@ __global__ __launch_bounds__(whole_block<Op>()) void k_rows_whole(const float *_
     T acc[4] = {Op::identity(), Op::identity(), Op::identity(), Op::identity()};
 #pragma unroll
     for (int u = 0; u < UNR; ++u) fold4<Op>(acc, v[u], 4 * (tid + u * NT), 1, k4);
+    if (tid == 0) first_nan_fix<Op>(acc[0], v[0].x);
     T r = Op::combine(Op::combine(acc[0], acc[1]), Op::combine(acc[2], acc[3]));
     r = wave_reduce<Op>(r);
     if ((tid & (kWave - 1)) == 0) lds[tid / kWave] = r;
@@ -528,6 +525,7 @@ __global__ __launch_bounds__(kBlock) void k_rows_bytes(const float *__restrict__
         if constexpr (Op::kShift) e = e - k;
         acc = Op::accum(acc, e, static_cast<int>(i));
     }
+    if (threadIdx.x == 0) first_nan_fix<Op>(acc, xr[0]);
     acc = block_reduce<Op, kBlock>(acc, lds);
     if (threadIdx.x == 0) write_out<Op>(out, row, acc);
 }
@@ -627,6 +625,15 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
                 }
                 for (; r < r1; r += NW) fold4<Op>(acc, ld4_stream(xc + r * inner), static_cast<int>(r), 0, k4);
             }
+            if constexpr (std::is_same_v<T, ArgPair>) {
+                if (r0 == 0 && w == 0) {  // row 0 of these four columns
+                    const float4 x0 = ld4(xc);
+                    first_nan_fix<Op>(acc[0], x0.x);
+                    first_nan_fix<Op>(acc[1], x0.y);
+                    first_nan_fix<Op>(acc[2], x0.z);
+                    first_nan_fix<Op>(acc[3], x0.w);
+                }
+            }
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) lds[w][lane * 4 + c] = acc[c];
@@ -642,6 +649,7 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
                 if constexpr (Op::kShift) v = v - k;
                 mine = Op::accum(mine, v, static_cast<int>(r));
             }
+            if (r0 == 0 && ph == 0) first_nan_fix<Op>(mine, xo[col]);
         }
         lds[ph][c] = mine;
     }

@@ -16,6 +16,7 @@
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "cxm_common.hpp"
 
@@ -23,28 +24,87 @@ namespace {
 
 int st(hipError_t e) { return e == hipSuccess ? CXM_OK : static_cast<int>(e); }
 
+// One device region of a stream's scratch.  `pinned`: handed to a launch
+// made under stream capture, so a graph holds its address; it is then never
+// freed while the entry lives (a growth retires it instead) and goes back to
+// the device only with the stream (cxm_stream_destroy) or at
+// cxm_release_workspaces.
+struct Region {
+    void *p = nullptr;
+    size_t size = 0;  // counters (workspace), rows (exchange) or slots (tagged)
+    size_t bytes = 0;
+    bool pinned = false;
+};
+
 struct WsEntry {
-    void *base = nullptr;
-    size_t counters = 0;
-    size_t scratch_bytes = 0;
-    void *xbase = nullptr;  // exchange region (never shared with other kernels' scratch)
-    size_t xrows = 0;
-    void *tbase = nullptr;  // tagged partial slots (never shared either)
-    size_t tslots = 0;
-    unsigned tepoch = 0;    // tag of the last call that used them
+    Region ws;       // ticket counters + partials
+    size_t ws_counters = 0, ws_scratch = 0;
+    Region xc;       // exchange region (never shared with other kernels' scratch)
+    Region tg;       // tagged partial slots (never shared either)
+    std::vector<void *> retired;  // pinned regions replaced by a growth
 };
 
 void free_entry(WsEntry &w) {
-    if (w.base) (void)hipFree(w.base);
-    if (w.xbase) (void)hipFree(w.xbase);
-    if (w.tbase) (void)hipFree(w.tbase);
-    w.base = w.xbase = w.tbase = nullptr;
+    for (Region *r : {&w.ws, &w.xc, &w.tg}) {
+        if (r->p) (void)hipFree(r->p);
+        *r = Region{};
+    }
+    for (void *p : w.retired) (void)hipFree(p);
+    w.retired.clear();
 }
 
 std::atomic<unsigned> g_xwait{1u << 16};
+// Tags of the flat reductions' slots, one counter for the whole process: a
+// region freed by one stream and handed to another by the allocator can
+// hold no slot with a tag a later call uses (until 2^32 calls have passed).
+std::atomic<unsigned> g_tag{0};
 
 std::mutex g_ws_mu;
 std::map<std::pair<int, cxm_stream_t>, WsEntry> g_ws;
+
+// Whether s is capturing (any capture status but none).
+int capturing(cxm_stream_t s, bool *cap) {
+    hipStreamCaptureStatus c = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(reinterpret_cast<hipStream_t>(s), &c);
+    if (e != hipSuccess) return st(e);
+    *cap = c != hipStreamCaptureStatusNone;
+    return CXM_OK;
+}
+
+// Makes r a zero-filled region of `bytes` (recording `size`), replacing a
+// smaller one.  Under capture nothing is allocated, filled or synchronised
+// (a hipMemsetAsync would only be recorded into the graph, not run):
+// CXM_E_CAPTURE, and the caller makes one eager call of that shape first.
+// A replaced region the stream's queued kernels may still use is waited
+// for; a pinned one is kept (a captured graph holds its address).
+int grow(WsEntry &w, Region &r, size_t size, size_t bytes, bool cap, cxm_stream_t s) {
+    if (cap) return CXM_E_CAPTURE;
+    hipStream_t hs = reinterpret_cast<hipStream_t>(s);
+    if (r.p != nullptr) {
+        const hipError_t e = hipStreamSynchronize(hs);
+        if (e != hipSuccess) return st(e);
+        if (r.pinned) {
+            w.retired.push_back(r.p);
+        } else {
+            const hipError_t f = hipFree(r.p);
+            if (f != hipSuccess) return st(f);
+        }
+        r = Region{};
+    }
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return st(e);
+    e = hipMemsetAsync(p, 0, bytes, hs);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return st(e);
+    }
+    r.p = p;
+    r.size = size;
+    r.bytes = bytes;
+    r.pinned = false;
+    return CXM_OK;
+}
 
 }  // namespace
 
@@ -56,38 +116,28 @@ int get_workspace(cxm_stream_t s, size_t counters, size_t scratch_bytes, Workspa
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return st(e);
+    bool cap = false;
+    int rc = capturing(s, &cap);
+    if (rc) return rc;
     std::lock_guard<std::mutex> lk(g_ws_mu);
     WsEntry &w = g_ws[{dev, s}];
-    if (w.base == nullptr || w.counters < counters || w.scratch_bytes < scratch_bytes) {
+    if (w.ws.p == nullptr || w.ws_counters < counters || w.ws_scratch < scratch_bytes) {
         size_t nc = counters < 1024 ? 1024 : counters;
         size_t sb = scratch_bytes < (size_t(8) << 20) ? (size_t(8) << 20) : scratch_bytes;
-        if (w.counters > nc) nc = w.counters;
-        if (w.scratch_bytes > sb) sb = w.scratch_bytes;
+        if (w.ws_counters > nc) nc = w.ws_counters;
+        if (w.ws_scratch > sb) sb = w.ws_scratch;
         const size_t cw = nc * cxm::kCtr;  // words; a multiple of 64 keeps the scratch 256-byte aligned
-        if (w.base != nullptr) {
-            // Kernels queued on this stream may still use the old region.
-            e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(s));
-            if (e != hipSuccess) return st(e);
-            e = hipFree(w.base);
-            w.base = nullptr;
-            if (e != hipSuccess) return st(e);
-        }
-        void *p = nullptr;
-        e = hipMalloc(&p, cw * sizeof(unsigned) + sb);
-        if (e != hipSuccess) return st(e);
-        e = hipMemsetAsync(p, 0, cw * sizeof(unsigned), reinterpret_cast<hipStream_t>(s));
-        if (e != hipSuccess) {
-            (void)hipFree(p);
-            return st(e);
-        }
-        w.base = p;
-        w.counters = nc;
-        w.scratch_bytes = sb;
+        // only the counters need zeros; the fill covers the region's start
+        rc = grow(w, w.ws, nc, cw * sizeof(unsigned) + sb, cap, s);
+        if (rc) return rc;
+        w.ws_counters = nc;
+        w.ws_scratch = sb;
     }
-    ws->counters = static_cast<unsigned *>(w.base);
-    ws->counters_n = w.counters;
-    ws->scratch = static_cast<unsigned *>(w.base) + w.counters * cxm::kCtr;
-    ws->scratch_bytes = w.scratch_bytes;
+    if (cap) w.ws.pinned = true;
+    ws->counters = static_cast<unsigned *>(w.ws.p);
+    ws->counters_n = w.ws_counters;
+    ws->scratch = static_cast<unsigned *>(w.ws.p) + w.ws_counters * cxm::kCtr;
+    ws->scratch_bytes = w.ws_scratch;
     return CXM_OK;
 }
 
@@ -95,34 +145,22 @@ int get_exchange(cxm_stream_t s, size_t rows, Exchange *x) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return st(e);
+    bool cap = false;
+    int rc = capturing(s, &cap);
+    if (rc) return rc;
     std::lock_guard<std::mutex> lk(g_ws_mu);
     WsEntry &w = g_ws[{dev, s}];
-    if (w.xbase == nullptr || w.xrows < rows) {
+    if (w.xc.p == nullptr || w.xc.size < rows) {
         size_t nr = rows < 64 ? 64 : rows;
-        if (w.xrows > nr) nr = w.xrows;
-        if (w.xbase != nullptr) {
-            e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(s));
-            if (e != hipSuccess) return st(e);
-            e = hipFree(w.xbase);
-            w.xbase = nullptr;
-            w.xrows = 0;
-            if (e != hipSuccess) return st(e);
-        }
-        const size_t bytes = nr * (kCtr * sizeof(unsigned) + kXMaxSegs * 2 * sizeof(unsigned long long));
-        void *p = nullptr;
-        e = hipMalloc(&p, bytes);
-        if (e != hipSuccess) return st(e);
+        if (w.xc.size > nr) nr = w.xc.size;
         // all-zero: epoch 0, tickets 0, every slot tagged 0
-        e = hipMemsetAsync(p, 0, bytes, reinterpret_cast<hipStream_t>(s));
-        if (e != hipSuccess) {
-            (void)hipFree(p);
-            return st(e);
-        }
-        w.xbase = p;
-        w.xrows = nr;
+        const size_t bytes = nr * (kCtr * sizeof(unsigned) + kXMaxSegs * 2 * sizeof(unsigned long long));
+        rc = grow(w, w.xc, nr, bytes, cap, s);
+        if (rc) return rc;
     }
-    x->hdr = static_cast<unsigned *>(w.xbase);
-    x->slots = reinterpret_cast<unsigned long long *>(static_cast<unsigned *>(w.xbase) + w.xrows * kCtr);
+    if (cap) w.xc.pinned = true;
+    x->hdr = static_cast<unsigned *>(w.xc.p);
+    x->slots = reinterpret_cast<unsigned long long *>(static_cast<unsigned *>(w.xc.p) + w.xc.size * kCtr);
     return CXM_OK;
 }
 
@@ -130,40 +168,64 @@ int get_tagged(cxm_stream_t s, size_t n, TaggedSlots *t) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return st(e);
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    e = hipStreamIsCapturing(reinterpret_cast<hipStream_t>(s), &cap);
-    if (e != hipSuccess) return st(e);
+    bool cap = false;
+    int rc = capturing(s, &cap);
+    if (rc) return rc;
     std::lock_guard<std::mutex> lk(g_ws_mu);
     WsEntry &w = g_ws[{dev, s}];
-    if (w.tbase == nullptr || w.tslots < n) {
+    if (w.tg.p == nullptr || w.tg.size < n) {
         size_t nn = n < 4096 ? 4096 : n;
-        if (w.tslots > nn) nn = w.tslots;
-        if (w.tbase != nullptr) {
-            e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(s));
-            if (e != hipSuccess) return st(e);
-            e = hipFree(w.tbase);
-            w.tbase = nullptr;
-            w.tslots = 0;
-            if (e != hipSuccess) return st(e);
-        }
-        const size_t bytes = nn * sizeof(unsigned long long);
-        void *p = nullptr;
-        e = hipMalloc(&p, bytes);
-        if (e != hipSuccess) return st(e);
+        if (w.tg.size > nn) nn = w.tg.size;
         // all-zero: every slot tagged 0, a tag no call uses
-        e = hipMemsetAsync(p, 0, bytes, reinterpret_cast<hipStream_t>(s));
-        if (e != hipSuccess) {
-            (void)hipFree(p);
-            return st(e);
-        }
-        w.tbase = p;
-        w.tslots = nn;
+        rc = grow(w, w.tg, nn, nn * sizeof(unsigned long long), cap, s);
+        if (rc) return rc;
     }
-    if (++w.tepoch == 0) w.tepoch = 1;
-    t->slots = static_cast<unsigned long long *>(w.tbase);
-    t->n = w.tslots;
-    t->epoch = w.tepoch;
-    t->clear = cap != hipStreamCaptureStatusNone ? 1 : 0;
+    if (cap) w.tg.pinned = true;
+    t->slots = static_cast<unsigned long long *>(w.tg.p);
+    t->n = w.tg.size;
+    t->epoch = next_tag();
+    t->clear = cap ? 1 : 0;
+    return CXM_OK;
+}
+
+unsigned next_tag() {
+    unsigned v = g_tag.fetch_add(1u, std::memory_order_relaxed) + 1u;
+    while (v == 0u || v == ~0u)  // 0 marks an empty slot; ~0 is tag 0's miss mark
+        v = g_tag.fetch_add(1u, std::memory_order_relaxed) + 1u;
+    return v;
+}
+
+int device_layout(DevLayout *out) {
+    static std::atomic<int> cus[64], xccs[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return st(e);
+    if (dev < 0 || dev >= 64) return CXM_E_TOO_LARGE;
+    int c = cus[dev].load(std::memory_order_acquire), x = xccs[dev].load(std::memory_order_relaxed);
+    if (c == 0) {
+        e = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return st(e);
+        e = hipDeviceGetAttribute(&x, hipDeviceAttributeNumberOfXccs, dev);
+        if (e != hipSuccess || x < 1) x = 1;
+        xccs[dev].store(x, std::memory_order_relaxed);
+        cus[dev].store(c, std::memory_order_release);
+    }
+    out->cus = c;
+    out->xccs = x;
+    return CXM_OK;
+}
+
+int workspace_query(cxm_stream_t s, int which, void **base, size_t *bytes, int *pinned) {
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return st(e);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    auto it = g_ws.find({dev, s});
+    const Region none{};
+    const Region &r = it == g_ws.end() ? none : which == 0 ? it->second.ws : which == 1 ? it->second.xc : it->second.tg;
+    *base = r.p;
+    *bytes = r.bytes;
+    *pinned = r.pinned ? 1 : 0;
     return CXM_OK;
 }
 
@@ -179,6 +241,9 @@ const char *cxm_error_string(int status) {
         case CXM_E_INVALID: return "invalid argument (null pointer, bad size or enum)";
         case CXM_E_TOO_LARGE: return "size beyond the kernel's index range";
         case CXM_E_NO_DEVICE: return "no gfx950 device";
+        case CXM_E_CAPTURE:
+            return "stream is capturing and the call needs scratch the stream does not have yet "
+                   "(make one eager call of that shape on the stream before capture)";
         default:
             if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
             return "unknown cxm status";
@@ -314,6 +379,11 @@ int cxm_event_destroy(cxm_event_t e) {
     return st(hipEventDestroy(reinterpret_cast<hipEvent_t>(e)));
 }
 
+int cxm_workspace_query(cxm_stream_t s, int which, void **base, size_t *bytes, int *pinned) {
+    if (!base || !bytes || !pinned || which < 0 || which > 2) return CXM_E_INVALID;
+    return cxm::workspace_query(s, which, base, bytes, pinned);
+}
+
 int cxm_exchange_wait_limit(unsigned polls, unsigned *previous) {
     const unsigned old = g_xwait.exchange(polls);
     if (previous) *previous = old;
@@ -327,11 +397,9 @@ int cxm_release_workspaces(void) {
     (void)hipGetDevice(&cur);
     for (auto &kv : g_ws) {
         (void)hipSetDevice(kv.first.first);
-        hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(kv.first.second));
-        if (e == hipSuccess && kv.second.base) e = hipFree(kv.second.base);
-        if (e == hipSuccess && kv.second.xbase) e = hipFree(kv.second.xbase);
-        if (e == hipSuccess && kv.second.tbase) e = hipFree(kv.second.tbase);
+        const hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(kv.first.second));
         if (e != hipSuccess && rc == CXM_OK) rc = st(e);
+        if (e == hipSuccess) free_entry(kv.second);
     }
     g_ws.clear();
     (void)hipSetDevice(cur);

@@ -344,6 +344,13 @@ class Mlp3:
              _p(params["w2"]), _p(params["b2"]), _p(params["w3"]), _p(params["b3"]), float(lr),
              _p(loss), _s(stream))
 
+    def last_side(self):
+        """Side workgroups of the last step's paired weight-gradient launch
+        (0: the output layer's finish and the b1 step ran as kernels)."""
+        n = ctypes.c_uint(0)
+        call("cxm_mlp3_last_side", self._h, ctypes.byref(n))
+        return n.value
+
     def close(self):
         if self._h.value:
             call("cxm_mlp3_destroy", self._h)

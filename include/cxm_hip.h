@@ -37,6 +37,12 @@ typedef struct ihipEvent_t *cxm_event_t;   /* a hipEvent_t */
 #define CXM_E_INVALID (-1)     /* null pointer, zero/mismatched size, bad enum */
 #define CXM_E_TOO_LARGE (-2)   /* size beyond what the kernel indexes (int32 argmax etc.) */
 #define CXM_E_NO_DEVICE (-3)   /* no gfx950 device visible */
+/* The stream is capturing a HIP graph and the call needs scratch (the
+ * stream's workspace, exchange region or tagged slots) that the stream does
+ * not have yet, or not large enough: nothing was allocated, filled, waited
+ * for or launched.  Make one eager call of the same shapes on the stream
+ * before capture. */
+#define CXM_E_CAPTURE (-4)
 
 /* Binary operator codes (Engine/AVX2/broadcast.hpp:29-56, Engine/AVX2/matrix.hpp:38-94). */
 #define CXM_OP_ADD 0
@@ -105,8 +111,19 @@ int cxm_event_record(cxm_event_t e, cxm_stream_t s);
 int cxm_event_sync(cxm_event_t e);
 int cxm_event_elapsed_ms(float *ms, cxm_event_t start, cxm_event_t stop);
 int cxm_event_destroy(cxm_event_t e);
-/* Frees every workspace the library holds (waits for their streams first). */
+/* Frees every workspace the library holds (waits for their streams first).
+ * Scratch regions are per (device, stream) and only grow.  A region handed
+ * to a launch recorded under stream capture is pinned: a later growth keeps
+ * it allocated, so the graph stays valid; it is freed by
+ * cxm_release_workspaces or by cxm_stream_destroy of its stream, which end
+ * every graph captured on that stream.  Under capture a missing or too
+ * small region is CXM_E_CAPTURE (see above). */
 int cxm_release_workspaces(void);
+/* Diagnostics, no reference counterpart: the current device's scratch
+ * region `which` (0 workspace, 1 exchange region, 2 tagged slots) of
+ * stream s -- its base (NULL if none yet), size in bytes, and whether a
+ * captured launch holds it (pinned). */
+int cxm_workspace_query(cxm_stream_t s, int which, void **base, size_t *bytes, int *pinned);
 
 /* Stream-ordered caching allocator: the replacement for ForgeChunk
  * (Memory/forge.cuh:30-90, forge.cu:13-122), the device branch of
@@ -145,7 +162,22 @@ int cxm_pool_stats(cxm_pool_stats_t *stats);
  *   mean, flat: sum / (float)N; axis: the first floor(outer*inner/8)*8
  *       outputs are sum * rn(1/dim), the rest sum / (float)dim (reduce.cpp:77-83).
  * Sums are deterministic (fixed tree order) and differ from the reference's
- * 8-lane sequential order only in rounding. */
+ * 8-lane sequential order only in rounding.
+ * NaN and signed zeros (max, min, argmax, argmin, all forms):
+ *   max / min are IEEE 754-2019 maximum / minimum: the result is a quiet NaN
+ *       when any element is NaN, and a +0/-0 tie gives +0 (max) / -0 (min).
+ *       The reference's _mm256_max_ps / _mm256_min_ps fold (functions.hpp:
+ *       314-325) returns the later operand on a NaN or a tie, so its result
+ *       then depends on where the NaN or the zeros sit in its 8-lane order;
+ *       without NaN and +0/-0 ties the two are the same bit for bit.
+ *   argmax / argmin: NaN elements are skipped (no comparison selects them),
+ *       except a NaN first element of the row, column or flat array, which
+ *       gives index 0 -- the reference starts from that element and takes
+ *       only strictly greater (smaller) values after it (reduce.cpp:442-455,
+ *       483-521, 530-621); +0 and -0 compare equal, so the first of them wins.  This
+ *       is the reference's axis form exactly; its flat form agrees except
+ *       where a NaN inside an 8-element block makes it read the element 32
+ *       places on (horizontal.hpp:154-159: countr_zero of an empty mask). */
 int cxm_reduce_sum_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s);
 int cxm_reduce_mean_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s);
 int cxm_reduce_max_flat_f32(const float *x, float *z, size_t n, cxm_stream_t s);
@@ -404,6 +436,11 @@ int cxm_mlp3_step_f32(cxm_mlp3 *handle, const float *x, const int32_t *labels, f
                       float *w2, float *b2, float *w3, float *b3, float lr, float *loss,
                       cxm_stream_t s);
 int cxm_mlp3_destroy(cxm_mlp3 *handle);
+/* Diagnostics, no reference counterpart: how many workgroups of the last
+ * step's paired weight-gradient launch ran the output layer's finish and
+ * the layer-1 bias step on the CUs the products left free (0: they ran as
+ * kernels of their own). */
+int cxm_mlp3_last_side(const cxm_mlp3 *handle, unsigned *wgs);
 
 #ifdef __cplusplus
 }

@@ -215,3 +215,127 @@ def test_capture_softmax_gemm_mlp_step(hip):
         h.hipGraphDestroy(graph)
         net.close()
         s.close()
+
+
+def _query(stream, which):
+    base, nbytes, pinned = ctypes.c_void_p(), ctypes.c_size_t(), ctypes.c_int()
+    call("cxm_workspace_query", stream.handle, which, ctypes.byref(base), ctypes.byref(nbytes), ctypes.byref(pinned))
+    return base.value, nbytes.value, pinned.value
+
+
+def _allocated(h, ptr):
+    """hipPointerGetAttributes succeeds on a live device allocation only."""
+    attrs = (ctypes.c_char * 256)()
+    h.hipPointerGetAttributes.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    h.hipPointerGetAttributes.restype = ctypes.c_int
+    return h.hipPointerGetAttributes(attrs, ctypes.c_void_p(ptr)) == 0
+
+
+def test_capture_without_scratch_is_refused(hip):
+    """Under capture, a call that needs scratch its stream does not have
+    yet returns CXM_E_CAPTURE before allocating, filling, waiting for or
+    launching anything, and capture ends cleanly with an empty graph."""
+    from cortexmind_amd._lib import E_CAPTURE, lib
+
+    h = hip_rt()
+    s = Stream()
+    L = lib()
+    # x holds the largest input read here: the [4096, 4096] column sum and
+    # the 2^24-element flat sum (the [64, 131072] softmax reads the first half)
+    x = DeviceArray((1 << 24,), np.float32)
+    y = DeviceArray((64 * 131072,), np.float32)
+    z = DeviceArray((4096,), np.float32)
+    assert x.size >= max(1 << 24, 4096 * 4096, 64 * 131072)
+    try:
+        assert h.hipStreamBeginCapture(s.handle, CAPTURE_RELAXED) == 0
+        st = [
+            L.cxm_reduce_sum_flat_f32(x.ptr, z.ptr, 1 << 24, s.handle),          # tagged slots
+            L.cxm_reduce_sum_f32(x.ptr, z.ptr, 1, 4096, 4096, s.handle),        # workspace (column ticket)
+            L.cxm_softmax_fwd_f32(x.ptr, y.ptr, 64, 131072, 0, s.handle),       # exchange region
+        ]
+        graph = ctypes.c_void_p()
+        assert h.hipStreamEndCapture(s.handle, ctypes.byref(graph)) == 0
+        n = ctypes.c_size_t(99)
+        h.hipGraphGetNodes.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_size_t)]
+        h.hipGraphGetNodes.restype = ctypes.c_int
+        assert h.hipGraphGetNodes(graph, None, ctypes.byref(n)) == 0
+        h.hipGraphDestroy(graph)
+        assert st == [E_CAPTURE] * 3, st
+        assert n.value == 0
+        for which in (0, 1, 2):
+            assert _query(s, which)[0] is None  # nothing was allocated for this stream
+        # the same calls made eagerly afterwards work
+        call("cxm_reduce_sum_f32", x.ptr, z.ptr, 1, 4096, 4096, s.handle)
+        s.sync()
+        assert _query(s, 0)[0] is not None
+    finally:
+        s.close()
+
+
+def test_captured_workspace_survives_growth(hip):
+    """A region handed to a captured launch is pinned: a later eager call
+    that needs a larger workspace on the same stream gets a new region and
+    the old one stays allocated, so the graph still replays correctly."""
+    h = hip_rt()
+    s = Stream()
+    g = SplitMix64(0x6D)
+    x = DeviceArray((4096 * 4096,), np.float32)
+    z = DeviceArray((4096,), np.float32)
+    M, K, N = 1024, 4096, 1024  # split-K A^T B: 64 tiles x 4 splits of 128x128 partials (16 MiB)
+    ga, gb, gc = DeviceArray((K * M,), np.float32), DeviceArray((K * N,), np.float32), DeviceArray((M * N,), np.float32)
+    ga.upload(g.uniform((K * M,), -1.0, 1.0))
+    gb.upload(g.uniform((K * N,), -1.0, 1.0))
+
+    def red():
+        call("cxm_reduce_sum_f32", x.ptr, z.ptr, 1, 4096, 4096, s.handle)
+
+    x.upload(g.uniform((4096 * 4096,), -1.0, 1.0))
+    red()  # sizes the workspace (the default 8 MiB of partials)
+    s.sync()
+    base0, bytes0, pinned0 = _query(s, 0)
+    assert pinned0 == 0
+    graph, exe = capture(h, s, red)
+    try:
+        base1, bytes1, pinned1 = _query(s, 0)
+        assert (base1, bytes1, pinned1) == (base0, bytes0, 1)
+        call("cxm_gemm_f32", ga.ptr, gb.ptr, gc.ptr, M, K, N, 1, 0, None, 0, None, s.handle)  # grows it
+        s.sync()
+        base2, bytes2, pinned2 = _query(s, 0)
+        assert base2 != base0 and bytes2 > bytes0 and pinned2 == 0
+        assert _allocated(h, base0), "the pinned region was freed while a graph holds it"
+        for rep in range(3):
+            x.upload(g.uniform((4096 * 4096,), -1.0, 1.0))
+            red()
+            want = z.numpy(s).copy()
+            z.fill_bytes(0xFF, s)
+            assert h.hipGraphLaunch(exe, s.handle) == 0
+            assert z.numpy(s).tobytes() == want.tobytes(), rep
+    finally:
+        h.hipGraphExecDestroy(exe)
+        h.hipGraphDestroy(graph)
+        s.close()
+
+
+def test_tags_differ_across_streams(hip):
+    """Flat-reduction tags come from one process-wide counter: two streams'
+    calls interleaved never reuse a tag, and a region freed with one stream
+    and taken by another holds no slot that matches (checked through the
+    results: each stream's sums equal the eager bits on fresh data)."""
+    g = SplitMix64(0x6E)
+    n = 1 << 22
+    xs = [DeviceArray((n,), np.float32) for _ in range(2)]
+    zs = [DeviceArray((1,), np.float32) for _ in range(2)]
+    ref = DeviceArray((1,), np.float32)
+    for rep in range(4):
+        streams = [Stream(), Stream()]
+        data = [g.uniform((n,), -1.0, 1.0) for _ in range(2)]
+        for i in range(2):
+            xs[i].upload(data[i])
+        for i in range(2):
+            call("cxm_reduce_sum_flat_f32", xs[i].ptr, zs[i].ptr, n - rep, streams[i].handle)
+        for i in range(2):
+            streams[i].sync()
+            call("cxm_reduce_sum_noalloc_f32", xs[i].ptr, ref.ptr, 1, n - rep, 1, None)
+            assert zs[i].numpy(streams[i]).tobytes() == ref.numpy().tobytes(), (rep, i)
+        for st in streams:
+            st.close()

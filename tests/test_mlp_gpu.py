@@ -22,7 +22,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 FIX = np.load(os.path.join(HERE, "golden", "fixtures_f64.npz"))
 
 
-def gpu_steps(x, labels, params, lr, steps):
+def gpu_steps(x, labels, params, lr, steps, side=None):
+    """`steps` fused steps; with `side`, the number of side workgroups of
+    each step's paired weight-gradient launch goes into that list."""
     b, d0 = x.shape
     d1, d2, d3 = params["w1"].shape[1], params["w2"].shape[1], params["w3"].shape[1]
     net = engine.Mlp3(b, d0, d1, d2, d3)
@@ -32,6 +34,8 @@ def gpu_steps(x, labels, params, lr, steps):
     for _ in range(steps):
         net.step(dx, dlab, dp, lr, dloss)
         losses.append(float(dloss.numpy()[0]))
+        if side is not None:
+            side.append(net.last_side())
     net.close()
     return losses, {k: v.numpy() for k, v in dp.items()}
 
@@ -67,9 +71,13 @@ def test_mlp_full_size_ten_steps_vs_oracle(hip, orc):
     (about 3 s per step on one CPU core).  At this batch the weight gradients
     take the split-K kernels with the fused SGD epilogue, which the reduced
     batch does not reach.  Every step's loss within 1e-5 relative; all six
-    tensors after step 10 within 1e-4 of their scale."""
+    tensors after step 10 within 1e-4 of their scale.  The paired
+    weight-gradient launch leaves CUs free here, so its side workgroups run
+    the output layer's finish and the b1 step (asserted)."""
     x, labels, params = c5_mlp()
-    losses, final = gpu_steps(x, labels, params, 0.01, 10)
+    ran = []
+    losses, final = gpu_steps(x, labels, params, 0.01, 10, ran)
+    assert all(w > 0 for w in ran), ran
     ref = {k: v.copy() for k, v in params.items()}
     ref_losses = []
     for step in range(10):
@@ -91,23 +99,34 @@ def test_mlp_full_size_ten_steps_vs_oracle(hip, orc):
     assert all(np.isfinite(losses)) and losses[-1] < losses[0]
 
 
-@pytest.mark.parametrize("batch,dims", [(100, (49, 64, 36, 3)), (37, (20, 40, 1024, 16)), (300, (784, 128, 96, 10)),
-                                        (64, (16, 24, 1028, 10)), (16, (8, 8, 4, 1)), (40, (784, 256, 256, 10)),
-                                        (520, (784, 1024, 1024, 10))], ids=lambda v: str(v))
-def test_mlp_shapes_vs_oracle(hip, orc, batch, dims):
+@pytest.mark.parametrize("batch,dims,side", [
+    (100, (49, 64, 36, 3), False), (37, (20, 40, 1024, 16), False), (300, (784, 128, 96, 10), False),
+    (64, (16, 24, 1028, 10), False), (16, (8, 8, 4, 1), False), (40, (784, 256, 256, 10), False),
+    (520, (784, 1024, 1024, 10), False), (384, (784, 1024, 1024, 10), True), (640, (784, 1024, 1024, 10), True),
+    (384, (784, 256, 1024, 10), True)], ids=lambda v: str(v))
+def test_mlp_shapes_vs_oracle(hip, orc, batch, dims, side):
     """The fused output layer (d3 <= 16, d2 <= 1024, d2 % 4 == 0) at batch
     sizes off its 16-row tile, with 1, 3 and 16 classes and d2 from 4 to its
     1024 limit; d2 = 1028 takes the unfused kernels.  Batches of 40 and 520
-    (a partial last 16-row head tile, split-K weight gradients at 520) with
-    the paired launch's side workgroups running the head's finish and the
-    b1 step.  Random biases, three steps at lr 0.05 (0.01 at batch 520)
-    against the oracle's step, same bars as above."""
+    have a partial last 16-row head tile; their weight gradients (K = batch,
+    not a multiple of 128) take the unpaired kernels, and the output layer's
+    finish and the b1 step run as kernels of their own.  Batches of 384 and
+    640 (multiples of 128, not of 256) pair the weight gradients on the
+    ring, with split K at 640, and leave CUs free, so the paired launch's
+    side workgroups run the finish and the b1 step, the latter with a
+    partial last row tile of its 256-row column sums (rows >= batch
+    masked); `side` asserts which path ran.  Random biases, three steps at
+    lr 0.05 (0.01 from batch 384 on: at 0.05 the 1024-wide layers overshoot
+    and the loss rises at step 2) against the oracle's step, same bars as
+    above."""
     x, labels, params = c5_mlp(batch=batch, dims=dims)
     g = SplitMix64(77 + batch)
     for k in ("b1", "b2", "b3"):
         params[k] = g.normal(params[k].shape, 0.0, 0.1)
-    lr = 0.05 if batch < 512 else 0.01  # at 0.05 the 1024-wide layers overshoot (loss rises at step 2)
-    losses, final = gpu_steps(x, labels, params, lr, 3)
+    lr = 0.05 if batch < 384 else 0.01
+    ran = []
+    losses, final = gpu_steps(x, labels, params, lr, 3, ran)
+    assert all(w > 0 for w in ran) if side else all(w == 0 for w in ran), ran
     ref = {k: v.copy() for k, v in params.items()}
     ref_losses = [orc.mlp_step(x, labels, ref, lr) for _ in range(3)]
     for got, want in zip(losses, ref_losses):
@@ -130,7 +149,9 @@ def test_mlp_pair_without_free_cus_vs_oracle(hip, orc):
     g = SplitMix64(2048)
     for k in ("b1", "b2", "b3"):
         params[k] = g.normal(params[k].shape, 0.0, 0.1)
-    losses, final = gpu_steps(x, labels, params, 0.01, 3)
+    ran = []
+    losses, final = gpu_steps(x, labels, params, 0.01, 3, ran)
+    assert ran == [0, 0, 0], ran
     ref = {k: v.copy() for k, v in params.items()}
     ref_losses = [orc.mlp_step(x, labels, ref, 0.01) for _ in range(3)]
     for got, want in zip(losses, ref_losses):
