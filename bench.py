@@ -21,11 +21,21 @@ WRITE_SIZE, scaled against a plain copy kernel), read from
 profiles/pmc_traffic.txt when that file has a line for the kernel.
 ``measured_peaks`` (bandwidth headlines) gives the copy and read rates this
 part reaches at 1 GiB, with the value and the roofline figure as fractions
-of the read rate, beside ``frac_of_peak`` against the 8 TB/s specification.
+of the read rate, beside ``frac_of_peak`` against the 8 TB/s specification,
+and ``single_launch_floors``: one launch of this library's fastest
+streaming kernels at the ops' own sizes (a 64 MiB read; 32 MiB in + 32 MiB
+out; 64 MiB in + 32 MiB out), timed like the ops, with each C2 op's (and,
+under "workloads", each C4 op's) fraction of its floor.  Every op's
+``kernel`` label (``kernel_of``) is the name rocprofv3's trace prints.
 ``cpu_baseline`` times the C restatement of the reference AVX2 path
 (oracle/, one thread, as the reference is single-threaded) on the same host
 over a bounded sample of whole steps; each BASELINE workload under
 "workloads" (C1, C3, C4, C5) carries its own.
+
+C5's roofline is the whole training step (its FLOP over its time on the
+fp32 matrix peak); ``first_10_steps`` times the configured ten steps of a
+fresh network from an idle queue (first step and the other nine apart),
+before the warm-up steps that precede the steady-state figure.
 
 The default run also reports the other workloads (C1 softmax, C3 affine
 fwd/bwd, C4 long-row softmax fwd/bwd, C5 MLP training step, and "more":
@@ -71,7 +81,9 @@ def parse():
 
 
 class Op:
-    """One op of a step: fn(k) launches it on input rotation slot k."""
+    """One op of a step: fn(k) launches it on input rotation slot k.
+    `kernel` is the kernel's name as rocprofv3's trace prints it (without
+    spaces), or a description for an op of several kernels."""
 
     def __init__(self, name, kernel, fn, work, unit="B", peak=None):
         self.name, self.kernel, self.fn, self.work, self.unit = name, kernel, fn, work, unit
@@ -120,7 +132,7 @@ def wl_c1(E, D):
     nbuf = 128  # 2 MiB each: 256 MiB of inputs and 256 MiB of outputs rotate
     xs = [D.from_numpy(x) for _ in range(nbuf)]
     ys = [D((r, c)) for _ in range(nbuf)]
-    ops = [Op("softmax_fwd", "k_sm_fwd_wave<4,false>",
+    ops = [Op("softmax_fwd", "k_sm_fwd_wave<4,false,2>",
               lambda k: E.softmax.forward(xs[k % nbuf], ys[k % nbuf], r, c), 2 * 4 * x.size)]
     desc = {"workload": "C1 row softmax fp32 [512,1024] N(0,1)*4", "shape": [r, c],
             "rotating_input_buffers": nbuf,
@@ -141,11 +153,12 @@ def wl_c3(E, D):
     A = E.activation
     big = 4 * m * n
     ops = []
+    # kernel labels as the trace names them: the activation code is the template argument
     for act, nm in [(E.ACT_RELU, "relu"), (E.ACT_SIGMOID, "sigmoid"), (E.ACT_TANH, "tanh")]:
-        ops.append(Op(f"fwd_{nm}", f"k_rowmap4<AffineF<{nm}>>",
+        ops.append(Op(f"fwd_{nm}", f"k_rowmap4<AffineF<{act}>>",
                       lambda k, act=act: A.affine_fwd(dx_, ds_, db_, y_, m, n, act), 2 * big + 2 * 4 * n))
     for act, nm in [(E.ACT_RELU, "relu"), (E.ACT_SIGMOID, "sigmoid"), (E.ACT_TANH, "tanh")]:
-        ops.append(Op(f"bwd_{nm}", f"k_affine_bwd<{nm}>",
+        ops.append(Op(f"bwd_{nm}", f"k_affine_bwd<{act},true,1,4>",
                       lambda k, act=act: A.affine_bwd(dx_, ds_, y_, dy_, dX, dS, dB, m, n, act),
                       4 * big + 3 * 4 * n))
     desc = {"workload": "C3 Y=act(X*scale+bias) fp32 [8192,8192], fwd+bwd, act in relu/sigmoid/tanh",
@@ -166,10 +179,13 @@ def wl_c4(E, D):
     big = 4 * x.size
     S = E.softmax
     ops = [
-        Op("softmax_fwd", "k_sm_fwd_x", lambda k: S.forward(X[k % nset], Y[k % nset], r, c), 2 * big),
-        Op("logsoftmax_fwd", "k_sm_fwd_x<log>", lambda k: S.forward(X[k % nset], Y[k % nset], r, c, log=True), 2 * big),
-        Op("softmax_bwd", "k_sm_bwd_x", lambda k: S.backward(Y[k % nset], G[k % nset], dX[k % nset], r, c), 3 * big),
-        Op("logsoftmax_bwd", "k_sm_bwd_x<log>", lambda k: S.backward(Y[k % nset], G[k % nset], dX[k % nset], r, c, log=True), 3 * big),
+        Op("softmax_fwd", "k_sm_fwd_x<false>", lambda k: S.forward(X[k % nset], Y[k % nset], r, c), 2 * big),
+        Op("logsoftmax_fwd", "k_sm_fwd_x<true>", lambda k: S.forward(X[k % nset], Y[k % nset], r, c, log=True),
+           2 * big),
+        Op("softmax_bwd", "k_sm_bwd_x<false>", lambda k: S.backward(Y[k % nset], G[k % nset], dX[k % nset], r, c),
+           3 * big),
+        Op("logsoftmax_bwd", "k_sm_bwd_x<true>",
+           lambda k: S.backward(Y[k % nset], G[k % nset], dX[k % nset], r, c, log=True), 3 * big),
     ]
     desc = {"workload": "C4 long-row softmax/log-softmax fwd+bwd fp32 [64,131072] N(0,1)*8, 10% -inf",
             "shape": [r, c], "rotating_sets": nset}
@@ -186,11 +202,12 @@ def wl_c5(E, D):
     P = {k: D.from_numpy(v) for k, v in params.items()}
     loss = D((1,))
     net = E.Mlp3(B, d0, d1, d2, d3)
-    ops = [Op("mlp_step", "cxm_mlp3_step", lambda k: net.step(dx_, dl_, P, 0.01, loss),
+    ops = [Op("mlp_step", "the MLP step (11 kernels; the largest, k_gemm_ring_pair<false,false>, both weight "
+              "gradients with their SGD steps)", lambda k: net.step(dx_, dl_, P, 0.01, loss),
               MLP_FLOP_PER_STEP, unit="FLOP")]
-    # the step's largest GEMM alone, for the MFMA roofline
+    # the step's layer-2 forward GEMM alone (a per-op figure beside the step)
     h1, w2, h2 = D((B, d1)), P["w2"], D((B, d2))
-    gemm_op = Op("gemm_fwd_4096x1024x1024", "k_gemm_ring<NN>",
+    gemm_op = Op("gemm_fwd_4096x1024x1024", "k_gemm_ring<true,true,false>",
                  lambda k: E.gemm(h1, w2, h2, B, d1, d2), 2 * B * d1 * d2, unit="FLOP")
     desc = {"workload": "C5 MLP 784-1024-1024-10 fp32 train step, batch 4096, SGD lr 0.01",
             "flop_per_step": MLP_FLOP_PER_STEP}
@@ -222,11 +239,14 @@ def wl_more(E, D):
         fn = getattr(R, op)
         kern = {"min": "MinOp", "argmin": "ArgMinOp", "norm1": "AbsSumOp", "norm2": "SqSumOp",
                 "var": "Pow2Op", "stdv": "Pow2Op"}[op]
-        ops.append(Op(f"{op}_global", f"k_rows<{kern}>", rot(lambda b, fn=fn: fn(b, z1, n)), xb + 4))
-        wide = kern in ("ArgMinOp", "Pow2Op")  # 64-bit partials: whole rows 256 threads a row, general column kernel
+        wide = kern in ("ArgMinOp", "Pow2Op")  # 64-bit partials: the flat form combines by ticket (MODE 1),
+        # whole rows take 256 threads a row, columns the general kernel; the column min starts from slice 0
+        ops.append(Op(f"{op}_global", f"k_rows<{kern},8,{1 if wide else 2}>", rot(lambda b, fn=fn: fn(b, z1, n)),
+                      xb + 4))
         ops.append(Op(f"{op}_axis1", f"k_rows_whole<{kern},{4 if wide else 8}>",
                       rot(lambda b, fn=fn, z=z: fn(b, z, rows, cols, 1)), xb + 4 * rows))
-        ops.append(Op(f"{op}_axis0", f"k_cols<{kern}>" if wide else f"k_cols_whole<{kern}>",
+        ckern = "MinColOp" if kern == "MinOp" else kern
+        ops.append(Op(f"{op}_axis0", f"k_cols<{ckern},true,16,16,true>" if wide else f"k_cols_whole<{ckern}>",
                       rot(lambda b, fn=fn, z=z: fn(b, z, 1, rows, cols)), xb + 4 * cols))
     # a flat sum of 2^24 + 3 floats from a base 4 bytes past 16-byte
     # alignment (the unaligned head and the ragged tail are folded in by the
@@ -243,13 +263,13 @@ def wl_more(E, D):
     xs = [D.from_numpy(X) for _ in range(2)]
     ys = [D((big,), np.float32) for _ in range(2)]
     W = E.wise
-    for nm in ("sqrt", "exp", "sin", "erf"):
+    for nm, fname in (("sqrt", "FSqrt"), ("exp", "FExp"), ("sin", "FSin"), ("erf", "FErf")):
         f = getattr(W, nm)
-        ops.append(Op(f"wise_{nm}", "k_map4", lambda k, f=f: f(xs[k % 2], ys[k % 2], big), 8 * big))
-    ops.append(Op("wise_pow_scalar", "k_map4<ScalarF<POW>>", lambda k: W.pow(xs[k % 2], 2.5, ys[k % 2], big), 8 * big))
-    ops.append(Op("wise_pow_tensor", "k_zip4<BinF<POW>>", lambda k: W.pow(xs[k % 2], xs[(k + 1) % 2], ys[k % 2], big),
+        ops.append(Op(f"wise_{nm}", f"k_map4<{fname}>", lambda k, f=f: f(xs[k % 2], ys[k % 2], big), 8 * big))
+    ops.append(Op("wise_pow_scalar", "k_map4<ScalarF<6>>", lambda k: W.pow(xs[k % 2], 2.5, ys[k % 2], big), 8 * big))
+    ops.append(Op("wise_pow_tensor", "k_zip4<BinF<6>>", lambda k: W.pow(xs[k % 2], xs[(k + 1) % 2], ys[k % 2], big),
                   12 * big))
-    ops.append(Op("wise_lerp", "k_map4", lambda k: W.lerp(xs[k % 2], 3.0, 0.25, ys[k % 2], big), 8 * big))
+    ops.append(Op("wise_lerp", "k_map4<FLerp>", lambda k: W.lerp(xs[k % 2], 3.0, 0.25, ys[k % 2], big), 8 * big))
     desc = {"workload": "reductions min/argmin/norm1/norm2/var/stdv on fp32 [4096,4096] and elementwise "
                         "math on fp32 [8192,8192]", "ops": [o.name for o in ops]}
     return ops, desc, (bufs, rag, z1, zf, zi, xs, ys), x
@@ -277,7 +297,8 @@ def wl_g16(E, D):
         keep += [a, b, c]
         # the automatic choice for these NN shapes: the 256 ring at >= 128
         # tiles of 256x256, else the 128 ring (B read as stored by both)
-        kern = "k_gemm16_ring<256>" if (m // 256) * (n // 256) >= 128 else "k_gemm16_ring<128>"
+        tm = 256 if (m // 256) * (n // 256) >= 128 else 128
+        kern = f"k_gemm16_ring<{1 if dt == DT_BF16 else 2},{tm},false>"
         ops.append(Op(name, kern, lambda i, a=a, b=b, c=c, m=m, k=k, n=n, dt=dt: E.matrix_t.matmul_t(a, b, c, m, k, n, dt),
                       2 * m * n * k, unit="FLOP", peak=PEAK_BF16_TFLOPS))
     desc = {"workload": "bf16/fp16 matmul NN (8192^3 bf16 and fp16, 4096^3 and 4096x1024x1024 bf16)",
@@ -401,7 +422,9 @@ def rate(work, ms, unit):
 
 
 def read_traffic():
-    """kernel -> (fetch_bytes, write_bytes) per launch from profiles/pmc_traffic.txt."""
+    """kernel -> (fetch_bytes, write_bytes) per launch from
+    profiles/pmc_traffic.txt (kernel names without spaces; a `[grid=...]`
+    suffix is dropped, the first line of a name counts)."""
     path = os.path.join(ROOT, "profiles", "pmc_traffic.txt")
     out = {}
     if os.path.exists(path):
@@ -409,14 +432,78 @@ def read_traffic():
             parts = line.split()
             if len(parts) >= 3 and not line.startswith("#"):
                 try:
-                    out[parts[0]] = (float(parts[1]), float(parts[2]))
+                    out.setdefault(parts[0].split("[grid=")[0], (float(parts[1]), float(parts[2])))
                 except ValueError:
                     pass
     return out
 
 
+def stream_floors(E, D, Event, sync, launches=100):
+    """Single-launch floors at the headline's and C4's sizes, from this
+    library's fastest streaming kernels, each timed like an op (events
+    around `launches` back-to-back launches, inputs rotating over ten
+    buffers of 64 MiB): a 64 MiB read (the row sum of [4096, 4096],
+    k_rows_whole, 16 KiB output), a 32 MiB in / 32 MiB out copy (z = x * 1,
+    k_map4 in its 1 KiB-piece layout) and a 64 MiB in / 32 MiB out zip
+    (z = x + y, k_zip4).  Every launch pays the kernel boundary (about
+    1.1-1.2 us between one launch's last workgroup and the next one's
+    first) on top of its streaming time, as the ops do."""
+    from cortexmind_amd._lib import OP_ADD, OP_MUL, call
+
+    n, nbuf = 4096 * 4096, 10
+    half = n // 2
+    bufs = [D((n,)) for _ in range(nbuf)]
+    for b in bufs:
+        call("cxm_memset", b.ptr, 0, b.nbytes, None)
+    z = D((4096,))
+    defs = [
+        ("read_64MiB", "k_rows_whole<SumOp,8>", 4 * n + 4 * 4096,
+         lambda k: E.reduce.sum(bufs[k % nbuf], z, 4096, 4096, 1)),
+        ("copy_32MiB_in_32MiB_out", "k_map4<ScalarF<2>>", 8 * half,
+         lambda k: call("cxm_scalar_f32", bufs[k % nbuf].ptr, 1.0, bufs[(k + 5) % nbuf].ptr, half, OP_MUL, None)),
+        ("zip_64MiB_in_32MiB_out", "k_zip4<BinF<0>>", 12 * half,
+         lambda k: call("cxm_binary_f32", bufs[k % nbuf].ptr, bufs[k % nbuf].ptr + 4 * half,
+                        bufs[(k + 5) % nbuf].ptr, half, OP_ADD, None)),
+    ]
+    res = {}
+    for name, kern, nbytes, fn in defs:
+        ms = time_op(Op(name, kern, fn, nbytes), launches, Event, sync)
+        res[name] = {"avg_ms": round(ms, 5), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1), "kernel": kern,
+                     "bytes": nbytes}
+    del bufs, z
+    return res
+
+
+def frac_of_floor(per_op, ops_floor, floors):
+    """Each op's GB/s over its floor's GB/s."""
+    return {name: round(per_op[name]["GB/s"] / floors[f]["GB/s"], 4) for name, f in ops_floor.items()
+            if name in per_op}
+
+
+def cold_steps(ops, steps, Event, sync):
+    """`steps` whole steps from an idle queue with no warm-up before them
+    (the first call of each kernel loads it, and the first call of an op
+    may grow the stream's scratch): {total ms per step, first step ms, ms
+    per step of the rest}, from events between the steps."""
+    sync()
+    ev = [Event() for _ in range(steps + 1)]
+    ev[0].record()
+    for k in range(steps):
+        for o in ops:
+            o.fn(k)
+        ev[k + 1].record()
+    ev[-1].sync()
+    total = ev[0].elapsed_ms(ev[-1])
+    first = ev[0].elapsed_ms(ev[1])
+    for e in ev:
+        e.close()
+    return {"ms_per_step": round(total / steps, 5), "first_step_ms": round(first, 5),
+            "rest_ms_per_step": round((total - first) / (steps - 1), 5)}
+
+
 def run_workload(name, steps, warmup, E, D, Event, sync):
     ops, desc, keep, host = WORKLOADS[name](E, D)
+    cold = cold_steps(ops, 10, Event, sync) if name == "c5" else None
     total_ms = time_steps(ops, steps, warmup, Event, sync)
     step_work = sum(o.work for o in ops)
     unit = ops[0].unit
@@ -430,32 +517,34 @@ def run_workload(name, steps, warmup, E, D, Event, sync):
         ms = time_op(o, launches, Event, sync)
         per_op[o.name] = {"avg_ms": round(ms, 5), "TFLOP/s": round(rate(o.work, ms, o.unit), 2)}
     # dominant kernel: the one with the largest share of step time (C5: the
-    # step's largest GEMM, timed alone)
-    if not extra_ops:
-        by_kernel = {}
-        for o in ops:
-            by_kernel.setdefault(o.kernel, []).append(o)
-        kern, group = max(by_kernel.items(), key=lambda kv: sum(per_op[o.name]["avg_ms"] for o in kv[1]))
-        avg_ms = float(np.mean([per_op[o.name]["avg_ms"] for o in group]))
-        work = float(np.mean([o.work for o in group]))
-        dunit = group[0].unit
-    else:
-        dom = extra_ops[0]
-        kern, avg_ms, work, dunit = dom.kernel, per_op[dom.name]["avg_ms"], dom.work, dom.unit
+    # step itself, one op of 11 kernels)
+    by_kernel = {}
+    for o in ops:
+        by_kernel.setdefault(o.kernel, []).append(o)
+    kern, group = max(by_kernel.items(), key=lambda kv: sum(per_op[o.name]["avg_ms"] for o in kv[1]))
+    avg_ms = float(np.mean([per_op[o.name]["avg_ms"] for o in group]))
+    work = float(np.mean([o.work for o in group]))
+    dunit = group[0].unit
     achieved = rate(work, avg_ms, dunit)
     if dunit == "B":
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4)}
     else:
-        peak = (group[0] if not extra_ops else dom).peak or PEAK_FP32_TFLOPS
+        peak = group[0].peak or PEAK_FP32_TFLOPS
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
                 "unit": "TFLOP/s", "frac": round(achieved / peak, 4)}
-    tr = read_traffic().get(kern)
+    tr = read_traffic().get(kern.replace(" ", ""))
     roof.update({"traffic": (tr[0] + tr[1]) if tr else None, "kernel": kern,
                  "avg_launch_ms": round(avg_ms, 5), "algorithmic_per_launch": work})
+    if not tr:
+        roof["traffic_note"] = "no line for this kernel in profiles/pmc_traffic.txt"
     value = rate(step_work * steps, total_ms, unit)
-    return {"value": value, "unit": "GB/s" if unit == "B" else "TFLOP/s", "ms_per_step": total_ms / steps,
-            "config": desc, "roofline": roof, "per_op": per_op, "host": host}
+    out = {"value": value, "unit": "GB/s" if unit == "B" else "TFLOP/s", "ms_per_step": total_ms / steps,
+           "config": desc, "roofline": roof, "per_op": per_op, "host": host,
+           "kernel_of": {o.name: o.kernel for o in ops + extra_ops}}
+    if cold is not None:
+        out["first_10_steps"] = cold
+    return out
 
 
 def host_cpu():
@@ -611,13 +700,22 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16/f16" if args.workload == "g16" else "f32",
         "data": "synthetic",
         "config": head["config"], "roofline": head["roofline"], "per_op": head["per_op"],
-        "device": info,
+        "kernel_of": head["kernel_of"], "device": info,
     }
+    if "first_10_steps" in head:
+        out["first_10_steps"] = head["first_10_steps"]
+    floors = None
     if head["unit"] == "GB/s":
         out["frac_of_peak"] = round(head["value"] / PEAK_HBM_GBS, 4)
         mp = measured_peaks(E, D, Event, sync)
         mp["value_frac_of_read"] = round(head["value"] / mp["read_GBps"], 4)
         mp["roofline_frac_of_read"] = round(head["roofline"]["achieved"] / mp["read_GBps"], 4)
+        floors = stream_floors(E, D, Event, sync)
+        mp["single_launch_floors"] = floors
+        if args.workload == "c2":
+            # every C2 op reads 64 MiB once: its fraction of the 64 MiB read floor
+            mp["per_op_frac_of_read_floor"] = frac_of_floor(head["per_op"], {o: "read_64MiB"
+                                                                              for o in head["per_op"]}, floors)
         out["measured_peaks"] = mp
     if not args.no_cpu and head["host"] is not None:
         cb = cpu_baseline(args.workload, head["host"], args.cpu_seconds)
@@ -635,9 +733,17 @@ def main():
             r = run_workload(name, max(20, args.steps // 2), 100 if name == "c5" else 10, E, D, Event, sync)
             wl[name] = {"workload": r["config"]["workload"], "value": round(r["value"], 2),
                         "unit": r["unit"], "ms_per_step": round(r["ms_per_step"], 5),
-                        "roofline": r["roofline"], "per_op": r["per_op"]}
+                        "roofline": r["roofline"], "per_op": r["per_op"], "kernel_of": r["kernel_of"]}
             if r["unit"] == "GB/s" and "measured_peaks" in out:
                 wl[name]["frac_of_measured_copy"] = round(r["value"] / out["measured_peaks"]["copy_GBps"], 4)
+            if name == "c4" and floors:
+                # forward: 32 MiB in, 32 MiB out; backward: 64 MiB in, 32 MiB out
+                wl[name]["per_op_frac_of_floor"] = frac_of_floor(
+                    r["per_op"], {"softmax_fwd": "copy_32MiB_in_32MiB_out", "logsoftmax_fwd": "copy_32MiB_in_32MiB_out",
+                                  "softmax_bwd": "zip_64MiB_in_32MiB_out", "logsoftmax_bwd": "zip_64MiB_in_32MiB_out"},
+                    floors)
+            if "first_10_steps" in r:
+                wl[name]["first_10_steps"] = r["first_10_steps"]
             if "note" in r["config"]:
                 wl[name]["note"] = r["config"]["note"]
             if not args.no_cpu and name in ("c1", "c3", "c4", "c5"):

@@ -537,12 +537,40 @@ __device__ __forceinline__ bool last_block_ticket2(unsigned *counters, unsigned 
 // ------------------------------------------------------ streaming maps
 //
 // Elementwise kernels over n floats with 16-byte aligned pointers: one
-// float4 per thread, one 256-thread workgroup per 1024 floats, non-temporal
-// loads and stores, and the n % 4 tail done by the one thread just past the
-// last float4.  Measured on gfx950 at 256 MiB in + 256 MiB out: 6.9 TB/s,
-// where the same map as a grid-stride loop over 4096-16384 workgroups stays
-// at 5.0-6.4 TB/s and hipMemcpyAsync at 5.4 TB/s.  An output may alias an
-// input: each element is read and written by the same thread.
+// float4 per thread, 256-thread workgroups, non-temporal loads and stores,
+// and the n % 4 tail done by the one thread whose vector index is n / 4.
+// An output may alias an input: each element is read and written by the
+// same thread.
+//
+// Layout: the array is cut into 1 KiB pieces (one wave's 64 float4), and
+// the pieces into virtual rows of kPieceRow; workgroup b's four waves take
+// piece b % kPieceRow of virtual rows 4 (b / kPieceRow) + 0..3, the layout
+// of k_rowmap4 below.  Consecutive workgroups, which the dispatcher deals
+// to the XCDs in turn, read consecutive 1 KiB pieces.  Measured on gfx950
+// at 256 MiB in + 256 MiB out (events around back-to-back launches): a
+// workgroup of four consecutive pieces (4 KiB) 80.2-80.8 us, this layout
+// 78.2-78.5 us, one 64-thread workgroup per piece 78.7-79.2 us; two and four
+// float4 per thread 87.4-87.7 us; blocks regrouped so each XCD reads one
+// contiguous eighth 82.5 us; temporal loads and stores 87 us.  Two inputs
+// and one output: 122.2-122.6 against 117.1 us.
+constexpr size_t kPieceRow = 32;
+
+// Vector (float4, or 8 x 16-bit) index of this thread.
+__device__ __forceinline__ size_t stream_vec() {
+    const unsigned b = blockIdx.x, w = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+    const size_t piece = (static_cast<size_t>(b / kPieceRow) * kWavesPerBlock + w) * kPieceRow + b % kPieceRow;
+    return piece * kWave + lane;
+}
+// Workgroups that cover vector indices 0 .. nv (nv itself: the tail
+// thread) in that layout; 0 when beyond the grid.  Also a grid of at least
+// nv + 1 threads for kernels that index threads contiguously.
+inline unsigned stream_grid_for(size_t nv) {
+    const size_t pieces = nv / kWave + 1;
+    const size_t rows = (pieces + kWavesPerBlock * kPieceRow - 1) / (kWavesPerBlock * kPieceRow);
+    const size_t b = rows * kPieceRow;
+    return b > 0xffffffffu ? 0u : static_cast<unsigned>(b);
+}
+
 template <class F>
 __device__ __forceinline__ float4 map4(const F &f, float4 v) {
     return make_float4(f(v.x), f(v.y), f(v.z), f(v.w));
@@ -550,7 +578,7 @@ __device__ __forceinline__ float4 map4(const F &f, float4 v) {
 
 template <class F>
 __global__ __launch_bounds__(kBlock) void k_map4(F f, const float *x, float *z, size_t n) {
-    const size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const size_t i = stream_vec();
     const size_t n4 = n / 4;
     if (i < n4) {
         st4_stream(z + 4 * i, map4(f, ld4_stream(x + 4 * i)));
@@ -561,7 +589,7 @@ __global__ __launch_bounds__(kBlock) void k_map4(F f, const float *x, float *z, 
 
 template <class F>
 __global__ __launch_bounds__(kBlock) void k_zip4(F f, const float *x, const float *y, float *z, size_t n) {
-    const size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const size_t i = stream_vec();
     const size_t n4 = n / 4;
     if (i < n4) {
         const float4 a = ld4_stream(x + 4 * i), b = ld4_stream(y + 4 * i);
@@ -572,10 +600,7 @@ __global__ __launch_bounds__(kBlock) void k_zip4(F f, const float *x, const floa
 }
 
 // Workgroups for k_map4 / k_zip4 over n floats (0 when n is beyond the grid).
-inline unsigned map4_grid(size_t n) {
-    const size_t b = (n / 4) / kBlock + 1;
-    return b > 0xffffffffu ? 0u : static_cast<unsigned>(b);
-}
+inline unsigned map4_grid(size_t n) { return stream_grid_for(n / 4); }
 
 // Row-structured streaming map over a row-major [m, 4*n4] matrix: one
 // float4 per thread.  The four waves of workgroup b take four consecutive

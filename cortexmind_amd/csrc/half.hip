@@ -48,7 +48,7 @@ __device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
 
 template <int DT, class F>
 __global__ __launch_bounds__(kBlock) void k_map8(F f, const uint16_t *x, uint16_t *z, size_t n) {
-    const size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const size_t i = stream_vec();
     const size_t n8 = n / 8;
     if (i < n8) {
         float v[8];
@@ -63,7 +63,7 @@ __global__ __launch_bounds__(kBlock) void k_map8(F f, const uint16_t *x, uint16_
 
 template <int DT, class F>
 __global__ __launch_bounds__(kBlock) void k_zip8(F f, const uint16_t *x, const uint16_t *y, uint16_t *z, size_t n) {
-    const size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const size_t i = stream_vec();
     const size_t n8 = n / 8;
     if (i < n8) {
         float a[8], b[8];
@@ -132,10 +132,9 @@ __global__ __launch_bounds__(kBlock) void k_conv_any(const void *x, void *z, siz
 
 inline hipStream_t hs(cxm_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
-inline unsigned grid8(size_t n) {
-    const size_t b = (n / 8) / kBlock + 1;
-    return b > 0xffffffffu ? 0u : static_cast<unsigned>(b);
-}
+// k_map8 / k_zip8 over n 16-bit elements: 8 per thread, the streaming
+// maps' layout (stream_vec)
+inline unsigned grid8(size_t n) { return stream_grid_for(n / 8); }
 inline unsigned grid_any(size_t n) {
     size_t b = (n + kBlock - 1) / kBlock;
     const size_t cap = 256 * 16;
