@@ -394,13 +394,17 @@ def time_steps(ops, steps, warmup, Event, sync):
     return ms
 
 
-def time_op(op, launches, Event, sync, lead=4):
+def time_op(op, launches, Event, sync, lead=4, warm=30):
     """Average time of one op from events around `launches` back-to-back
-    launches of it alone (inputs rotating).  `lead` untimed launches are
-    queued just before the start event, so the timed launches begin on a
-    busy queue rather than after the host's first enqueue (which added up
-    to 0.8 us per launch to a 12 us kernel over 50 launches)."""
-    for k in range(2):
+    launches of it alone (inputs rotating).  `warm` untimed launches run
+    first: the first ~10 launches of an op after other work ran up to 14%
+    slower (C4 forward at [64, 131072]: 12.5 against 11.0 us over 100
+    launches after two warm-up calls; the same settles after a few).  `lead`
+    untimed launches are queued just before the start event, so the timed
+    launches begin on a busy queue rather than after the host's first
+    enqueue (which added up to 0.8 us per launch to a 12 us kernel over 50
+    launches)."""
+    for k in range(warm):
         op.fn(k)
     sync()
     t0, t1 = Event(), Event()
