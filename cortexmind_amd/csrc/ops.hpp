@@ -21,6 +21,42 @@ __device__ __forceinline__ float bin_t(float a, float b) {
     else return powf(a, b);
 }
 
+// tanh(t) by the classic two-range method (an odd polynomial near 0, the
+// exponential form beyond; e.g. W. J. Cody and W. Waite, Software Manual
+// for the Elementary Functions, 1980, ch. 13), with coefficients of our own:
+//  * |t| < 0.9: t + t^3 P(t^2), P of degree 5 fitted to (tanh(x) - x) / x^3
+//    for the relative error of tanh on [0, 0.9] (iteratively reweighted
+//    least squares toward minimax), Horner in fp32;
+//  * otherwise q = (1 - e) / (1 + e) with e = exp(-2|t|) = 2^(|t| C),
+//    C = fl(-2 / ln 2); the quotient is the hardware reciprocal times
+//    1 - e, refined by one Newton step on the exact residual
+//    (1 - q) - e - q e ((1 - q) - e is exact by Sterbenz for e <= 0.17), so
+//    only the last rounding and e's error (scaled by 2e / (1 - e^2) <= 0.42)
+//    remain.  |t| is clamped to 16 on that path (tanh rounds to 1 from 9.01
+//    on), so infinities give +-1 and NaN stays NaN.
+// Modelled in float64 with the exp2 and reciprocal estimates off by one ulp
+// either way: at most 1.38 ulp; measured on the device against float64 in
+// tests/test_elementwise_gpu.py.  No branches (the math library's tanhf
+// branches on |t|).
+__device__ __forceinline__ float tanh_f32(float t) {
+    const float ax = fabsf(t);
+    const float z = ax * ax;
+    float p = 0x1.56e070p-10f;
+    p = fmaf(p, z, -0x1.c2429ep-8f);
+    p = fmaf(p, z, 0x1.56a8d2p-6f);
+    p = fmaf(p, z, -0x1.b81fd0p-5f);
+    p = fmaf(p, z, 0x1.1101fap-3f);
+    p = fmaf(p, z, -0x1.555508p-2f);
+    const float small = fmaf(ax * z, p, ax);
+    const float a = ax > 16.0f ? 16.0f : ax;  // NaN stays NaN
+    const float e = __builtin_amdgcn_exp2f(a * -0x1.715476p+1f);
+    const float r0 = __builtin_amdgcn_rcpf(1.0f + e);
+    const float q0 = (1.0f - e) * r0;
+    const float res = fmaf(-e, q0, (1.0f - q0) - e);
+    const float q = fmaf(r0, res, q0);
+    return __builtin_copysignf(ax < 0.9f ? small : q, t);
+}
+
 // relu: functions.hpp:372-374; sigmoid: functions.hpp:405-411 (1/(1+exp(-x)));
 // tanh: functions.hpp:381-383; exp: functions.hpp:186-188.
 template <int ACT>
@@ -42,7 +78,7 @@ __device__ __forceinline__ float act(float t) {
         const float q0 = n * r0;
         const float res = fmaf(-q0, e, n - q0);
         return fmaf(r0, res, q0);
-    } else if constexpr (ACT == CXM_ACT_TANH) return tanhf(t);
+    } else if constexpr (ACT == CXM_ACT_TANH) return tanh_f32(t);
     else if constexpr (ACT == CXM_ACT_EXP) return expf(t);
     else return t;
 }

@@ -205,3 +205,27 @@ def test_act_bwd_bit_exact(hip, orc, act, n, off):
     d_y, d_dy, d_dx = dev(y, off), dev(dy, off), empty((n,), offset_floats=off)
     call("cxm_act_bwd_f32", d_y.ptr, d_dy.ptr, d_dx.ptr, n, act, None)
     assert bits_equal(d_dx.numpy(), orc.act_bwd(y, dy, act))
+
+
+def test_tanh_ranges(hip):
+    """tanh (the library's two-range form): dense around the polynomial /
+    exponential switch at |t| = 0.9 (every float within 4096 ulps of it),
+    uniform on [-1.5, 1.5], tiny and denormal arguments (tanh(t) = t), and
+    the special values: +-0 keep their sign, +-inf give +-1, NaN stays NaN."""
+    g = SplitMix64(0x7A2)
+    sweep = np.float32(0.9).view(np.int32) + np.arange(-4096, 4097, dtype=np.int32)
+    near = sweep.view(np.float32)
+    x = np.concatenate([near, -near, g.uniform((1 << 20,), -1.5, 1.5), g.uniform((1 << 16,), 1e-8, 1e-3),
+                        np.array([1e-38, -1e-38, 1e-45, -1e-45, 3e-41], np.float32)]).astype(np.float32)
+    dx, dz = dev(x), empty(x.shape)
+    call("cxm_unary_f32", dx.ptr, dz.ptr, x.size, ACT_TANH, None)
+    got = dz.numpy()
+    ref = f64_act(x, ACT_TANH)
+    assert np.all(ulp_dist(got, ref) <= 2), int(ulp_dist(got, ref).max())
+    sp = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 9.5, -9.5, 1e30, -1e30], np.float32)
+    dx, dz = dev(sp), empty(sp.shape)
+    call("cxm_unary_f32", dx.ptr, dz.ptr, sp.size, ACT_TANH, None)
+    got = dz.numpy()
+    assert got[0] == 0.0 and not np.signbit(got[0]) and got[1] == 0.0 and np.signbit(got[1])
+    assert got[2] == 1.0 and got[3] == -1.0 and np.isnan(got[4])
+    assert list(got[5:]) == [1.0, -1.0, 1.0, -1.0]
