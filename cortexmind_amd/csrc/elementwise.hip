@@ -29,7 +29,7 @@ __device__ __forceinline__ float bin(int op, float a, float b) {
         case CXM_OP_DIV: return a / b;
         case CXM_OP_MAX: return a > b ? a : b;
         case CXM_OP_MIN: return a < b ? a : b;
-        default: return powf(a, b);
+        default: return pow_f32(a, b);
     }
 }
 

@@ -170,3 +170,60 @@ def test_argument_errors(hip):
     assert lib().cxm_bcast_row_f32(d.ptr, d.ptr, d.ptr, 2, 2, OP_POW, None) == E_INVALID
     assert lib().cxm_gather_f32(d.ptr, 4, None, d.ptr, 4, None) == E_INVALID
     assert lib().cxm_wise_f32(d.ptr, d.ptr, 0, 0, None) == 0
+
+
+def test_pow_wide_range(hip):
+    """pow over the ranges where its logarithm must be carried in double-float:
+    |x| at the edges of the reduction interval (about 0.707 and 1.414) with
+    |y| up to 140, x from 1e-38 to 1e38, x near 1 with |y| up to 1000, and
+    subnormal results; finite results within 2 ulp of float64 (subnormal
+    ones in units of the subnormal spacing)."""
+    g = SplitMix64(0x90)
+    xs = [g.uniform((1 << 16,), 0.69, 0.72), g.uniform((1 << 16,), 1.40, 1.43),
+          (10.0 ** g.uniform((1 << 16,), -38.0, 38.0)).astype(np.float32), g.uniform((1 << 16,), 0.9, 1.1),
+          g.uniform((1 << 16,), 0.5, 2.0)]
+    ys = [g.uniform((1 << 16,), -140.0, 140.0), g.uniform((1 << 16,), -140.0, 140.0),
+          g.uniform((1 << 16,), -1.5, 1.5), g.uniform((1 << 16,), -1000.0, 1000.0),
+          g.uniform((1 << 16,), -200.0, -120.0)]
+    x = np.concatenate(xs).astype(np.float32)
+    y = np.concatenate(ys).astype(np.float32)
+    dx, dy, dz = dev(x), dev(y), empty(x.shape)
+    call("cxm_binary_f32", dx.ptr, dy.ptr, dz.ptr, x.size, OP_POW, None)
+    got = dz.numpy()
+    with np.errstate(over="ignore", under="ignore"):
+        ref64 = np.power(x.astype(np.float64), y.astype(np.float64))
+    ref = ref64.astype(np.float32)
+    fin = np.isfinite(ref) & (np.abs(ref64) < 3.4e38)
+    spacing = np.maximum(np.spacing(np.abs(ref[fin])).astype(np.float64), 2.0 ** -149)
+    err = np.abs(got[fin].astype(np.float64) - ref64[fin]) / spacing
+    assert err.max() <= 2.0, float(err.max())
+    big = ~fin & (ref64 > 0)
+    assert np.all(np.isinf(got[big])), "overflowing results must be +inf"
+
+
+def test_pow_special_value_table(hip):
+    """The IEEE / C99 special cases of pow, against numpy's float32 power
+    (the C library's powf): every pair from a set of zeros, ones,
+    infinities, NaN, integers (odd, even), non-integers and subnormals of
+    both signs."""
+    vals = np.array([0.0, -0.0, 1.0, -1.0, 2.0, -2.0, 0.5, -0.5, 3.0, -3.0, 2.5, -2.5, np.inf, -np.inf, np.nan,
+                     1e-40, -1e-40, 1e30, -1e30, 7.0, 2.0 ** 24, 2.0 ** 25 + 2.0], np.float32)
+    x = np.repeat(vals, vals.size)
+    y = np.tile(vals, vals.size)
+    dx, dy, dz = dev(x), dev(y), empty(x.shape)
+    call("cxm_binary_f32", dx.ptr, dy.ptr, dz.ptr, x.size, OP_POW, None)
+    got = dz.numpy()
+    with np.errstate(all="ignore"):
+        want = np.power(x, y)  # float32 powf
+    bad = []
+    for i in range(x.size):
+        a, b = got[i], want[i]
+        if np.isnan(b):
+            ok = np.isnan(a)
+        elif np.isinf(b) or b == 0:
+            ok = a == b and np.signbit(a) == np.signbit(b)
+        else:
+            ok = abs(float(a) - float(b)) <= 2 * float(np.spacing(np.abs(b)))
+        if not ok:
+            bad.append((float(x[i]), float(y[i]), float(a), float(b)))
+    assert not bad, bad[:10]
