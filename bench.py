@@ -77,7 +77,99 @@ def parse():
     p.add_argument("--copy-calibration", action="store_true",
                    help="first copy 64 MiB device-to-device three times (the known-size "
                         "kernel that scales FETCH_SIZE / WRITE_SIZE counters)")
+    p.add_argument("--summarize", nargs="+", metavar=("KIND", "CSV"),
+                   help="summarise rocprofv3 output instead of running: 'trace <kernel_trace.csv>' prints the "
+                        "per-kernel table of profiles/*_kernel_trace.md; 'pmc <counter_collection.csv>...' prints "
+                        "per-kernel FETCH_SIZE / WRITE_SIZE bytes per launch scaled by the 64 MiB copy "
+                        "(profiles/pmc_traffic.txt lines); 'mfma <counter_collection.csv>' prints per-kernel "
+                        "MFMA busy from SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_MFMA and GRBM_GUI_ACTIVE")
     return p.parse_args()
+
+
+# ------------------------------------------------------- rocprof summaries
+
+def kernel_name(raw):
+    """A kernel's name as bench.py labels it: no return type, namespaces,
+    argument list or spaces."""
+    import re
+
+    n = re.sub(r"^void ", "", raw)
+    n = n.replace("cxm::(anonymous namespace)::", "").replace("(anonymous namespace)::", "").replace("cxm::", "")
+    depth, out = 0, []
+    for ch in n:  # drop the argument list: the first '(' outside template brackets
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            break
+        out.append(ch)
+    return "".join(out).replace(" ", "")
+
+
+def summarize(kind, paths):
+    import csv
+    from collections import OrderedDict
+
+    if kind == "trace":
+        g = OrderedDict()
+        for r in csv.DictReader(open(paths[0])):
+            grid = r.get("Grid_Size") or (int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]))
+            key = (kernel_name(r["Kernel_Name"]), int(grid))
+            g.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+        tot = sum(sum(v) for v in g.values())
+        print("| kernel | grid (threads) | calls | avg us | min us | max us | % time |")
+        print("|---|---:|---:|---:|---:|---:|---:|")
+        for (k, grid), v in sorted(g.items(), key=lambda kv: -sum(kv[1])):
+            print(f"| `{k}` | {grid} | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} | "
+                  f"{100 * sum(v) / tot:.1f} |")
+        return
+    if kind == "mfma":
+        # per dispatch: SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_MFMA, GRBM_GUI_ACTIVE (one row per counter)
+        disp, meta = {}, {}
+        for r in csv.DictReader(open(paths[0])):
+            k = int(r["Dispatch_Id"])
+            disp.setdefault(k, {})[r["Counter_Name"]] = float(r["Counter_Value"])
+            meta[k] = (kernel_name(r["Kernel_Name"]), int(r["Grid_Size"]))
+        g = OrderedDict()
+        for k, c in disp.items():
+            g.setdefault(meta[k], []).append(c)
+        print("| kernel | grid (threads) | dispatches | cycles per XCD | MFMA busy cycles / MFMA | MFMA busy |")
+        print("|---|---:|---:|---:|---:|---:|")
+        tot = lambda cs, n: sum(c.get(n, 0.0) for c in cs)  # noqa: E731
+        for (k, grid), cs in sorted(g.items(), key=lambda kv: -tot(kv[1], "SQ_VALU_MFMA_BUSY_CYCLES")):
+            mb, mi, ga = tot(cs, "SQ_VALU_MFMA_BUSY_CYCLES"), tot(cs, "SQ_INSTS_MFMA"), tot(cs, "GRBM_GUI_ACTIVE")
+            if mi == 0:
+                continue
+            # GRBM_GUI_ACTIVE sums the 8 XCDs' busy cycles; 1024 SIMDs in all
+            print(f"| `{k}` | {grid} | {len(cs)} | {ga / len(cs) / 8:.3g} | {mb / mi:.0f} | {100 * mb / (ga / 8 * 1024):.1f}% |")
+        return
+    if kind != "pmc":
+        raise SystemExit(f"unknown summary kind {kind}")
+    per = {}  # (name, grid) -> {counter: [bytes per dispatch]}
+    calib = {}  # counter -> [(dispatch id, bytes)] of the copies
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            c = r["Counter_Name"]
+            if c not in ("FETCH_SIZE", "WRITE_SIZE"):
+                continue
+            key = (kernel_name(r["Kernel_Name"]), int(r["Grid_Size"]))
+            v = float(r["Counter_Value"]) * 1024.0  # KiB
+            per.setdefault(key, {}).setdefault(c, []).append(v)
+            if key[0].startswith("__amd_rocclr_copyBuffer"):
+                calib.setdefault(c, []).append((int(r["Dispatch_Id"]), v))
+    scale = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        first = [v for _, v in sorted(calib.get(c, []))[:3]]  # --copy-calibration's copies run first
+        scale[c] = (64 * 2 ** 20) / (sum(first) / len(first)) if first else 1.0
+    print(f"# scale FETCH_SIZE x{scale['FETCH_SIZE']:.4f}, WRITE_SIZE x{scale['WRITE_SIZE']:.4f} "
+          "(a 64 MiB device-to-device copy reads and writes 64 MiB)")
+    for (k, grid), d in sorted(per.items(), key=lambda kv: (kv[0][0], -len(next(iter(kv[1].values()))))):
+        if k.startswith("__amd_rocclr"):
+            continue
+        f = sum(d.get("FETCH_SIZE", [0])) / max(1, len(d.get("FETCH_SIZE", []))) * scale["FETCH_SIZE"]
+        w = sum(d.get("WRITE_SIZE", [0])) / max(1, len(d.get("WRITE_SIZE", []))) * scale["WRITE_SIZE"]
+        print(f"{k}[grid={grid}] {f:.0f} {w:.0f}")
 
 
 class Op:
@@ -202,12 +294,16 @@ def wl_c5(E, D):
     P = {k: D.from_numpy(v) for k, v in params.items()}
     loss = D((1,))
     net = E.Mlp3(B, d0, d1, d2, d3)
-    ops = [Op("mlp_step", "the MLP step (11 kernels; the largest, k_gemm_ring_pair<false,false>, both weight "
+    ops = [Op("mlp_step", "the MLP step (5 kernels; the largest, k_gemm_ring_pair<false,false>, both weight "
               "gradients with their SGD steps)", lambda k: net.step(dx_, dl_, P, 0.01, loss),
               MLP_FLOP_PER_STEP, unit="FLOP")]
-    # the step's layer-2 forward GEMM alone (a per-op figure beside the step)
-    h1, w2, h2 = D((B, d1)), P["w2"], D((B, d2))
-    gemm_op = Op("gemm_fwd_4096x1024x1024", "k_gemm_ring<true,true,false>",
+    # the step's layer-2 forward GEMM alone (a per-op figure beside the step),
+    # on an h1 like the step's (ReLU of N(0, 1): half zeros): the MFMA clock
+    # depends on the data (power), so an all-zero operand would time faster
+    rng = np.random.default_rng(5)
+    h1 = D.from_numpy(np.maximum(rng.standard_normal((B, d1), dtype=np.float32), 0.0))
+    w2, h2 = P["w2"], D((B, d2))
+    gemm_op = Op("gemm_fwd_4096x1024x1024", "k_gemm_ring<true,false,false>",
                  lambda k: E.gemm(h1, w2, h2, B, d1, d2), 2 * B * d1 * d2, unit="FLOP")
     desc = {"workload": "C5 MLP 784-1024-1024-10 fp32 train step, batch 4096, SGD lr 0.01",
             "flop_per_step": MLP_FLOP_PER_STEP}
@@ -521,7 +617,7 @@ def run_workload(name, steps, warmup, E, D, Event, sync):
         ms = time_op(o, launches, Event, sync)
         per_op[o.name] = {"avg_ms": round(ms, 5), "TFLOP/s": round(rate(o.work, ms, o.unit), 2)}
     # dominant kernel: the one with the largest share of step time (C5: the
-    # step itself, one op of 11 kernels)
+    # step itself, one op of five kernels)
     by_kernel = {}
     for o in ops:
         by_kernel.setdefault(o.kernel, []).append(o)
@@ -661,6 +757,9 @@ def cpu_baseline(name, host, seconds):
 
 def main():
     args = parse()
+    if args.summarize:
+        summarize(args.summarize[0], args.summarize[1:])
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on one GPU only (every GPU box here has one); "
                                    "--gpus must be 1", "n_gpus": args.gpus}))
