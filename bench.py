@@ -82,7 +82,8 @@ def parse():
                         "per-kernel table of profiles/*_kernel_trace.md; 'pmc <counter_collection.csv>...' prints "
                         "per-kernel FETCH_SIZE / WRITE_SIZE bytes per launch scaled by the 64 MiB copy "
                         "(profiles/pmc_traffic.txt lines); 'mfma <counter_collection.csv>' prints per-kernel "
-                        "MFMA busy from SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_MFMA and GRBM_GUI_ACTIVE")
+                        "MFMA busy from SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_MFMA and GRBM_GUI_ACTIVE; 'tcc <counter_collection.csv>' "
+                        "per-kernel L2 hits and misses from TCC_HIT_sum and TCC_MISS_sum")
     return p.parse_args()
 
 
@@ -144,6 +145,25 @@ def summarize(kind, paths):
             # GRBM_GUI_ACTIVE sums the 8 XCDs' busy cycles; 1024 SIMDs in all
             print(f"| `{k}` | {grid} | {len(cs)} | {ga / len(cs) / 8:.3g} | {mb / mi:.0f} | {100 * mb / (ga / 8 * 1024):.1f}% |")
         return
+    if kind == "tcc":
+        disp, meta = {}, {}
+        for r in csv.DictReader(open(paths[0])):
+            k = int(r["Dispatch_Id"])
+            disp.setdefault(k, {})[r["Counter_Name"]] = float(r["Counter_Value"])
+            meta[k] = (kernel_name(r["Kernel_Name"]), int(r["Grid_Size"]))
+        g = OrderedDict()
+        for k, c in disp.items():
+            g.setdefault(meta[k], []).append(c)
+        print("| kernel | grid (threads) | dispatches | TCC_HIT | TCC_MISS | misses x 128 B | hit rate |")
+        print("|---|---:|---:|---:|---:|---:|---:|")
+        for (k, grid), cs in sorted(g.items(), key=lambda kv: kv[0]):
+            if k.startswith("__amd_rocclr"):
+                continue
+            h = sum(c.get("TCC_HIT_sum", 0.0) for c in cs) / len(cs)
+            m = sum(c.get("TCC_MISS_sum", 0.0) for c in cs) / len(cs)
+            print(f"| `{k}` | {grid} | {len(cs)} | {h:.0f} | {m:.0f} | {m * 128 / 2 ** 20:.2f} MiB | "
+                  f"{100 * h / max(1.0, h + m):.1f}% |")
+        return
     if kind != "pmc":
         raise SystemExit(f"unknown summary kind {kind}")
     per = {}  # (name, grid) -> {counter: [bytes per dispatch]}
@@ -175,11 +195,13 @@ def summarize(kind, paths):
 class Op:
     """One op of a step: fn(k) launches it on input rotation slot k.
     `kernel` is the kernel's name as rocprofv3's trace prints it (without
-    spaces), or a description for an op of several kernels."""
+    spaces), or a description for an op of several kernels, whose names
+    (one launch each per op) are then `parts`."""
 
-    def __init__(self, name, kernel, fn, work, unit="B", peak=None):
+    def __init__(self, name, kernel, fn, work, unit="B", peak=None, parts=None):
         self.name, self.kernel, self.fn, self.work, self.unit = name, kernel, fn, work, unit
         self.peak = peak  # TFLOP/s of the matrix unit this op runs on (FLOP ops); fp32 when None
+        self.parts = parts
 
 
 # ---------------------------------------------------------------- workloads
@@ -296,7 +318,9 @@ def wl_c5(E, D):
     net = E.Mlp3(B, d0, d1, d2, d3)
     ops = [Op("mlp_step", "the MLP step (5 kernels; the largest, k_gemm_ring_pair<false,false>, both weight "
               "gradients with their SGD steps)", lambda k: net.step(dx_, dl_, P, 0.01, loss),
-              MLP_FLOP_PER_STEP, unit="FLOP")]
+              MLP_FLOP_PER_STEP, unit="FLOP",
+              parts=["k_gemm_ring<true,false,true>", "k_gemm_ring<true,false,false>", "k_mlp_head",
+                     "k_gemm_ring<true,true,false>", "k_gemm_ring_pair<false,false>"])]
     # the step's layer-2 forward GEMM alone (a per-op figure beside the step),
     # on an h1 like the step's (ReLU of N(0, 1): half zeros): the MFMA clock
     # depends on the data (power), so an all-zero operand would time faster
@@ -633,7 +657,12 @@ def run_workload(name, steps, warmup, E, D, Event, sync):
         peak = group[0].peak or PEAK_FP32_TFLOPS
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
                 "unit": "TFLOP/s", "frac": round(achieved / peak, 4)}
-    tr = read_traffic().get(kern.replace(" ", ""))
+    known = read_traffic()
+    if group[0].parts:  # an op of several kernels: the sum of its kernels' lines
+        lines = [known.get(k) for k in group[0].parts]
+        tr = (sum(t[0] for t in lines), sum(t[1] for t in lines)) if all(lines) else None
+    else:
+        tr = known.get(kern.replace(" ", ""))
     roof.update({"traffic": (tr[0] + tr[1]) if tr else None, "kernel": kern,
                  "avg_launch_ms": round(avg_ms, 5), "algorithmic_per_launch": work})
     if not tr:
