@@ -51,3 +51,61 @@ def test_headline_line(hip):
     assert c["kind"] == "port" and c["cores"] == 1 and c["unit"] == "GB/s" and c["value"] > 0 and c["sample"]
     m = out["measured_peaks"]
     assert 1000.0 < m["read_GBps"] < 8000.0 and 1000.0 < m["copy_GBps"] < 8000.0
+
+
+def test_kernel_name_matches_bench_labels():
+    """rocprofv3's demangled names reduce to the labels bench.py uses."""
+    sys.path.insert(0, ROOT)
+    from bench import kernel_name
+
+    assert kernel_name("void cxm::(anonymous namespace)::k_cols<cxm::ArgMaxOp, true, 16, 16, true>"
+                       "(float const*, unsigned long, unsigned long, unsigned int)") == "k_cols<ArgMaxOp,true,16,16,true>"
+    assert kernel_name("void cxm::k_map4<cxm::(anonymous namespace)::ScalarF<2> >(cxm::(anonymous namespace)::"
+                       "ScalarF<2>, float const*, float*, unsigned long)") == "k_map4<ScalarF<2>>"
+    assert kernel_name("cxm::(anonymous namespace)::k_mlp_head(float const*, float const*)") == "k_mlp_head"
+    assert kernel_name("__amd_rocclr_copyBuffer") == "__amd_rocclr_copyBuffer"
+
+
+def _write_csv(path, header, rows):
+    import csv
+
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(header)
+        w.writerows(rows)
+
+
+def test_summarize_pmc_scales_by_the_first_copies(tmp_path):
+    """Counter values (KiB) scale so that the three calibration copies, the
+    first copyBuffer dispatches, read and write 64 MiB; later copies do not
+    change the factor."""
+    hdr = ["Dispatch_Id", "Grid_Size", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    fetch = [[1, 131072, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 32768.0],
+             [2, 131072, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 32768.0],
+             [3, 131072, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 32768.0],
+             [4, 1024, "void cxm::k_map4<cxm::FExp>(cxm::FExp, float const*, float*, unsigned long)", "FETCH_SIZE", 1024.0],
+             [5, 131072, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 524288.0]]
+    write = [[1, 131072, "__amd_rocclr_copyBuffer", "WRITE_SIZE", 65536.0],
+             [2, 131072, "__amd_rocclr_copyBuffer", "WRITE_SIZE", 65536.0],
+             [3, 131072, "__amd_rocclr_copyBuffer", "WRITE_SIZE", 65536.0],
+             [4, 1024, "void cxm::k_map4<cxm::FExp>(cxm::FExp, float const*, float*, unsigned long)", "WRITE_SIZE", 512.0]]
+    _write_csv(tmp_path / "f.csv", hdr, fetch)
+    _write_csv(tmp_path / "w.csv", hdr, write)
+    p = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--summarize", "pmc", str(tmp_path / "f.csv"),
+                        str(tmp_path / "w.csv")], cwd=ROOT, capture_output=True, text=True, timeout=60)
+    assert p.returncode == 0, p.stderr
+    lines = [ln for ln in p.stdout.splitlines() if not ln.startswith("#")]
+    assert lines == ["k_map4<FExp>[grid=1024] 2097152 524288"]  # 1024 KiB x 2, 512 KiB x 1
+
+
+def test_summarize_trace_table(tmp_path):
+    hdr = ["Kernel_Name", "Start_Timestamp", "End_Timestamp", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z"]
+    name = "void cxm::(anonymous namespace)::k_rows_whole<cxm::SumOp, 8>(float const*, unsigned long)"
+    _write_csv(tmp_path / "t.csv", hdr, [[name, 1000, 12000, 512, 1, 1], [name, 20000, 33000, 512, 1, 1],
+                                         ["k_other", 0, 1000, 64, 2, 1]])
+    p = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--summarize", "trace", str(tmp_path / "t.csv")],
+                       cwd=ROOT, capture_output=True, text=True, timeout=60)
+    assert p.returncode == 0, p.stderr
+    rows = [ln for ln in p.stdout.splitlines() if ln.startswith("| `")]
+    assert rows[0] == "| `k_rows_whole<SumOp,8>` | 512 | 2 | 12.00 | 11.00 | 13.00 | 96.0 |"
+    assert rows[1] == "| `k_other` | 128 | 1 | 1.00 | 1.00 | 1.00 | 4.0 |"
