@@ -77,6 +77,10 @@ def parse():
     p.add_argument("--copy-calibration", action="store_true",
                    help="first copy 64 MiB device-to-device three times (the known-size "
                         "kernel that scales FETCH_SIZE / WRITE_SIZE counters)")
+    p.add_argument("--timeline", action="store_true",
+                   help="instead of the bench line, print per-workgroup timelines of the C2 row sum, column sum, "
+                        "global sum and column argmax from the diagnostics build cortexmind_amd/"
+                        "libcxm_hip_timeline.so (make -C cortexmind_amd/csrc timeline)")
     p.add_argument("--summarize", nargs="+", metavar=("KIND", "CSV"),
                    help="summarise rocprofv3 output instead of running: 'trace <kernel_trace.csv>' prints the "
                         "per-kernel table of profiles/*_kernel_trace.md; 'pmc <counter_collection.csv>...' prints "
@@ -190,6 +194,97 @@ def summarize(kind, paths):
         f = sum(d.get("FETCH_SIZE", [0])) / max(1, len(d.get("FETCH_SIZE", []))) * scale["FETCH_SIZE"]
         w = sum(d.get("WRITE_SIZE", [0])) / max(1, len(d.get("WRITE_SIZE", []))) * scale["WRITE_SIZE"]
         print(f"{k}[grid={grid}] {f:.0f} {w:.0f}")
+
+
+# ------------------------------------------------------- C2 timelines
+
+TL_KINDS, TL_WGS, TL_MARKS = 4, 4096, 4  # reduce.hip's timeline tables
+
+
+def timeline(reps=40):
+    """C2's row sum, column sum, global sum and column argmax launched back to
+    back `reps` times (inputs rotating over ten 64 MiB buffers), then the
+    diagnostics build's per-workgroup marks of the last round, in us from the
+    round's first workgroup start: 0 entry, 1 all waves' loads folded, 2 partial
+    published (column ticket taken, or flat tagged slot stored), 3 final
+    store issued (the last workgroup of a column tile, the flat reader)."""
+    import ctypes
+
+    from cortexmind_amd import _lib
+
+    _lib.LIB_PATH = os.path.join(ROOT, "cortexmind_amd", "libcxm_hip_timeline.so")
+    from cortexmind_amd import engine as E
+    from cortexmind_amd._lib import call, lib
+    from cortexmind_amd.data import c2_reduce
+    from cortexmind_amd.device import DeviceArray as D
+
+    x = c2_reduce()
+    rows, cols = x.shape
+    bufs = [D.from_numpy(x) for _ in range(10)]
+    z1, zf, zi = D((1,), np.float32), D((cols,), np.float32), D((cols,), np.int32)
+    R = E.reduce
+    ops = [("row sum", "k_rows_whole<SumOp,8>", 0, lambda b: R.sum(b, zf, rows, cols, 1)),
+           ("column sum", "k_cols_whole<SumOp>", 1, lambda b: R.sum(b, zf, 1, rows, cols)),
+           ("global sum", "k_rows<SumOp,8,2>", 2, lambda b: R.sum(b, z1, rows * cols)),
+           ("column argmax", "k_cols<ArgMaxOp,true,16,16,true>", 3, lambda b: R.argmax(b, zi, 1, rows, cols))]
+    k = 0
+    for _ in range(reps):
+        for _, _, _, fn in ops:
+            fn(bufs[k % len(bufs)])
+            k += 1
+    call("cxm_device_sync")
+    t = np.zeros((TL_KINDS, TL_WGS, TL_MARKS), np.uint64)
+    fn = lib().cxm_timeline_read
+    fn.argtypes, fn.restype = [ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int
+    if fn(t.ctypes.data, t.size) != 0:
+        raise RuntimeError("cxm_timeline_read failed")
+    timeline_report(t, [(name, kern, kind) for name, kern, kind, _ in ops], {0: rows, 1: 256, 2: 2049, 3: 256})
+
+
+def timeline_report(t, ops, grids):
+    """Prints timeline()'s tables from the raw marks t [kinds, wgs, marks];
+    `ops` lists (name, kernel, kind) in launch order, `grids` the workgroups
+    per launch of each kind."""
+    t = t.astype(np.int64)
+    recs = {kind: t[kind, :grids[kind]] for _, _, kind in ops}
+    t0 = min(int(r[:, 0][r[:, 0] > 0].min()) for r in recs.values())
+    us = lambda v: (np.asarray(v, dtype=np.float64) - t0) / 100.0  # noqa: E731  (100 MHz clock)
+    print("| op (kernel) | workgroups | first start | last start | loads folded: median / last | "
+          "last partial published | end | combine after the last fold | gap to the next op |")
+    print("|---|---:|---:|---:|---:|---:|---:|---:|---:|")
+    lines = []
+    for name, kern, kind in ops:
+        r = recs[kind]
+        start, fold, pub, fin = r[:, 0], r[:, 1], r[:, 2], r[:, 3]
+        if kind == 2:  # the flat sum: writers 0..2047, the reader last
+            wfold, wpub = fold[:-1], pub[:-1]
+            end = fin[-1]
+            last_pub = wpub.max()
+            fold_med, fold_max = np.median(wfold), wfold.max()
+        elif kind == 0:
+            end = fin.max()
+            last_pub = None
+            fold_med, fold_max = np.median(fold), fold.max()
+        else:  # column tiles: the last workgroup of each writes the result
+            ends = np.where(fin > start, fin, pub)
+            end = ends.max()
+            last_pub = pub.max()
+            fold_med, fold_max = np.median(fold), fold.max()
+        lines.append([name, kern, r.shape[0], us(start.min()), us(start.max()), us(fold_med), us(fold_max),
+                      us(last_pub) if last_pub is not None else None, us(end), start.min(), end, fold_max])
+    for i, ln in enumerate(lines):
+        gap = (lines[i + 1][9] - ln[10]) / 100.0 if i + 1 < len(lines) else None
+        print(f"| {ln[0]} (`{ln[1]}`) | {ln[2]} | {ln[3]:.2f} | {ln[4]:.2f} | {ln[5]:.2f} / {ln[6]:.2f} | "
+              + (f"{ln[7]:.2f}" if ln[7] is not None else "—") + f" | {ln[8]:.2f} | {(ln[10] - ln[11]) / 100.0:.2f} | "
+              + (f"{gap:.2f}" if gap is not None else "—") + " |")
+    print()
+    print("| op | loads folded, last workgroup by XCD 0..7 (us from the op's first start) |")
+    print("|---|---|")
+    for (name, _, kind), ln in zip(ops, lines):
+        r = recs[kind][:-1] if kind == 2 else recs[kind]
+        xcd = np.arange(r.shape[0]) % 8
+        per = [(r[xcd == c, 1].max() - ln[9]) / 100.0 for c in range(8)]
+        print(f"| {name} | " + " ".join(f"{v:.2f}" for v in per) + " |")
 
 
 class Op:
@@ -788,6 +883,9 @@ def main():
     args = parse()
     if args.summarize:
         summarize(args.summarize[0], args.summarize[1:])
+        return
+    if args.timeline:
+        timeline()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on one GPU only (every GPU box here has one); "

@@ -39,6 +39,31 @@ constexpr size_t kFixedZeroBytes = kFixedCounterBytes + kFixedTaggedBytes;  // c
 static __device__ __align__(256) unsigned char scratch[kFixedZeroBytes + kFixedPartBytes];
 static_assert(kFixedZeroBytes % 256 == 0, "partials stay 256-byte aligned");
 
+// Per-workgroup timeline of the C2 kernels, for the diagnostics build only
+// (`make -C cortexmind_amd/csrc timeline`: this file compiled with
+// -DCXM_TIMELINE into libcxm_hip_timeline.so; `bench.py --timeline` reads
+// it).  Thread 0 of a workgroup writes the 100 MHz s_memrealtime clock to
+// mark i of its record in table `kind`: 0 entry, 1 all its waves' loads
+// folded (past the workgroup's first barrier after them), 2 its partial
+// published (ticket taken, or tagged slot stored), 3 the last workgroup's
+// (or the reader's) final store issued.  Records are indexed by
+// the linear workgroup id modulo kTimelineWgs; a launch overwrites the
+// previous launch's records of its kind.  Without CXM_TIMELINE the marks
+// compile to nothing.
+enum TimelineKind : unsigned { kTlRows = 0, kTlCols = 1, kTlFlat = 2, kTlColsArg = 3 };
+#ifdef CXM_TIMELINE
+constexpr unsigned kTimelineKinds = 4, kTimelineWgs = 4096, kTimelineMarks = 4;
+static __device__ unsigned long long timeline[kTimelineKinds][kTimelineWgs][kTimelineMarks];
+__device__ __forceinline__ void tl_mark(unsigned kind, unsigned i) {
+    if (threadIdx.x == 0) {
+        const unsigned wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+        __builtin_nontemporal_store(__builtin_amdgcn_s_memrealtime(), &timeline[kind][wg % kTimelineWgs][i]);
+    }
+}
+#else
+__device__ __forceinline__ void tl_mark(unsigned, unsigned) {}
+#endif
+
 namespace cxm {
 namespace {
 
@@ -292,6 +317,7 @@ __global__ __launch_bounds__(whole_block<Op>()) void k_rows_whole(const float *_
     constexpr int NT = whole_block<Op>(), NW = NT / kWave;
     __shared__ T lds[NW];
     const int tid = threadIdx.x;
+    tl_mark(kTlRows, 0);
     const float *__restrict__ xr = x + static_cast<size_t>(blockIdx.x) * dim;
     float k = 0.0f;
     if constexpr (Op::kShift) k = xr[0];
@@ -308,12 +334,14 @@ __global__ __launch_bounds__(whole_block<Op>()) void k_rows_whole(const float *_
     r = wave_reduce<Op>(r);
     if ((tid & (kWave - 1)) == 0) lds[tid / kWave] = r;
     __syncthreads();
+    tl_mark(kTlRows, 1);
     if (tid == 0) {  // waves in order
         T a = lds[0];
 #pragma unroll
         for (int w = 1; w < NW; ++w) a = Op::combine(a, lds[w]);
         write_out<Op>(out, blockIdx.x, a);
     }
+    tl_mark(kTlRows, 3);
 }
 
 // Reductions over the last axis: workgroup b reduces segment b % segs of
@@ -361,6 +389,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
         constexpr bool CLEAR = MODE == 3;
         constexpr int IT = kMaxFlatSegs / kBlock;
         if (blockIdx.x == segs) {  // the reader
+            tl_mark(kTlFlat, 0);
             // The first loads are unconditional (the slot regions hold at
             // least kMaxFlatSegs entries): a load in a branch makes the
             // compiler wait for it at the branch's end, serialising the
@@ -441,6 +470,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
                         for (int w = 1; w < kWavesPerBlock; ++w) r = Op::combine(r, lds[w]);
                         write_out<Op>(out, 0, r);
                     }
+                    tl_mark(kTlFlat, 3);
                     return;
                 }
                 __syncthreads();  // lds is reused below
@@ -470,7 +500,9 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
             return;
         }
         // a writer
+        tl_mark(kTlFlat, 0);
         const T r = row_segment<Op, UNR, true>(x, dim, blockIdx.x, seg4, lds);
+        tl_mark(kTlFlat, 1);
         if (tid == 0) {
             const unsigned long long v = (static_cast<unsigned long long>(epoch) << 32) | __builtin_bit_cast(unsigned, r);
             if constexpr (CLEAR) {
@@ -484,6 +516,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(const float *__restrict__ x, si
                 __hip_atomic_store(slots + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
+        tl_mark(kTlFlat, 2);
         return;
     } else {
         // MODE 0 has one segment per row: no division ahead of the loads
@@ -570,6 +603,7 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
         o = q / ntiles;
     }
     const int tid = threadIdx.x;
+    tl_mark(kTlColsArg, 0);
     const float *__restrict__ xo = x + o * dim * inner;
     const size_t r0 = chunk * rows_per_chunk;
     const size_t r1 = r0 + rows_per_chunk < dim ? r0 + rows_per_chunk : dim;
@@ -654,6 +688,7 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
         lds[ph][c] = mine;
     }
     __syncthreads();
+    tl_mark(kTlColsArg, 1);
     const bool owner = tid < kColTile;  // threads 0..255 own one column each from here
     T mine = Op::identity();
     if (owner) {
@@ -668,11 +703,14 @@ __global__ __launch_bounds__(NW * kWave) void k_cols(const float *__restrict__ x
     }
     const size_t slot = (o * ntiles + tile) * chunks;
     if (owner) st_dev(&part[(slot + chunk) * kColTile + tid], mine);
-    if (!last_block_ticket(ctr(counters, o * ntiles + tile), chunks, &flag)) return;
+    const bool last = last_block_ticket(ctr(counters, o * ntiles + tile), chunks, &flag);
+    tl_mark(kTlColsArg, 2);
+    if (!last) return;
     if (owner) {
         const T a = combine_partials<Op>(part + slot * kColTile + tid, chunks, kColTile, Op::identity());
         if (FAST || col < inner) write_out<Op>(out, o * inner + col, a);
     }
+    tl_mark(kTlColsArg, 3);
 }
 
 // Column chunks of exactly 256 rows over whole 256-column tiles (C2's
@@ -693,6 +731,7 @@ __global__ __launch_bounds__(16 * kWave) void k_cols_whole(const float *__restri
     __shared__ int flag;
     const unsigned chunk = blockIdx.x, tile = blockIdx.y, o = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    tl_mark(kTlCols, 0);
     const unsigned w = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(tid / kWave));
     const float *__restrict__ xo = x + o * slice + static_cast<size_t>(tile) * kColTile;
     // this wave's first row of the chunk: row chunk * 256 + w, then every 16th
@@ -711,6 +750,7 @@ __global__ __launch_bounds__(16 * kWave) void k_cols_whole(const float *__restri
 #pragma unroll
     for (int c = 0; c < 4; ++c) lds[w][lane * 4 + c] = acc[c];
     __syncthreads();
+    tl_mark(kTlCols, 1);
     const bool owner = tid < kColTile;
     T mine = Op::identity();
     if (owner) {
@@ -720,11 +760,14 @@ __global__ __launch_bounds__(16 * kWave) void k_cols_whole(const float *__restri
     }
     const size_t slot = (static_cast<size_t>(o) * ntiles + tile) * chunks;
     if (owner) st_dev(&part[(slot + chunk) * kColTile + tid], mine);
-    if (!last_block_ticket(ctr(counters, static_cast<size_t>(o) * ntiles + tile), chunks, &flag)) return;
+    const bool last = last_block_ticket(ctr(counters, static_cast<size_t>(o) * ntiles + tile), chunks, &flag);
+    tl_mark(kTlCols, 2);
+    if (!last) return;
     if (owner) {
         const T a = combine_partials<Op>(part + slot * kColTile + tid, chunks, kColTile, Op::identity());
         write_out<Op>(out, static_cast<size_t>(o) * inner + static_cast<size_t>(tile) * kColTile + tid, a);
     }
+    tl_mark(kTlCols, 3);
 }
 
 __global__ void k_fill_f32(float *z, float v) { *z = v; }
@@ -1013,6 +1056,17 @@ int colsum_sgd(const float *x, float *b, size_t rows, size_t cols, float lr, cxm
 }
 
 }  // namespace cxm
+
+#ifdef CXM_TIMELINE
+// Diagnostics build only (not declared in include/cxm_hip.h): copies the
+// timeline tables, kTimelineKinds x kTimelineWgs x kTimelineMarks 64-bit
+// words, to host memory (after the caller's synchronisation).
+extern "C" int cxm_timeline_read(unsigned long long *host, size_t words) {
+    if (!host || words != static_cast<size_t>(kTimelineKinds) * kTimelineWgs * kTimelineMarks) return CXM_E_INVALID;
+    const hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(timeline), words * sizeof(unsigned long long));
+    return e == hipSuccess ? CXM_OK : static_cast<int>(e);
+}
+#endif
 
 extern "C" {
 

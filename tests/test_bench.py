@@ -109,3 +109,34 @@ def test_summarize_trace_table(tmp_path):
     rows = [ln for ln in p.stdout.splitlines() if ln.startswith("| `")]
     assert rows[0] == "| `k_rows_whole<SumOp,8>` | 512 | 2 | 12.00 | 11.00 | 13.00 | 96.0 |"
     assert rows[1] == "| `k_other` | 128 | 1 | 1.00 | 1.00 | 1.00 | 4.0 |"
+
+
+def test_timeline_report_on_synthetic_marks(capsys):
+    """timeline_report's arithmetic on hand-made marks (100 MHz ticks): the
+    end of a column op is its last tile's final store, stale final marks
+    (earlier than the workgroup's start) are ignored, gaps run from one op's
+    end to the next op's first start."""
+    sys.path.insert(0, ROOT)
+    import numpy as np
+
+    from bench import TL_KINDS, TL_MARKS, TL_WGS, timeline_report
+
+    t = np.zeros((TL_KINDS, TL_WGS, TL_MARKS), np.uint64)
+    base = 10_000
+    # kind 0: 8 row workgroups, start 0..7 ticks, fold +1000, end +1100
+    for w in range(8):
+        t[0, w] = [base + w, base + w + 1000, 0, base + w + 1100]
+    # kind 1: 8 column workgroups starting 200 ticks after the rows' end
+    c0 = base + 7 + 1100 + 200
+    for w in range(8):
+        t[1, w] = [c0 + w, c0 + 1000 + w, c0 + 1100 + w, 5]  # final mark stale (earlier launch)
+    t[1, 7, 3] = c0 + 1300  # the last workgroup's final store
+    timeline_report(t, [("row sum", "k_r", 0), ("column sum", "k_c", 1)], {0: 8, 1: 8})
+    out = capsys.readouterr().out.splitlines()
+    row = [ln for ln in out if ln.startswith("| row sum")][0].split("|")
+    col = [ln for ln in out if ln.startswith("| column sum")][0].split("|")
+    assert row[3].strip() == "0.00" and row[4].strip() == "0.07"
+    assert row[7].strip() == "11.07"   # end: 7 + 1100 ticks
+    assert row[9].strip() == "2.00"    # gap to the column op: 200 ticks
+    assert col[7].strip() == f"{(c0 + 1300 - base) / 100:.2f}"
+    assert col[8].strip() == "2.93"    # combine after the last fold: 1300 - 1007 ticks
