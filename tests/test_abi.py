@@ -125,3 +125,18 @@ def test_pool_core_bookkeeping():
                          timeout=60)
     assert run.returncode == 0, run.stdout + run.stderr
     assert "ALL OK" in run.stdout
+
+
+def test_timeline_build_exports_its_reader():
+    """The diagnostics build (reduce.hip with -DCXM_TIMELINE, built beside the
+    library) carries gfx950 code and exports cxm_timeline_read; the library
+    itself does not."""
+    import os
+
+    path = os.path.join(os.path.dirname(_lib.LIB_PATH), "libcxm_hip_timeline.so")
+    if not os.path.exists(path):
+        pytest.skip("diagnostics build not built (make -C cortexmind_amd/csrc timeline)")
+    tl = ctypes.CDLL(path)
+    assert hasattr(tl, "cxm_timeline_read")
+    assert b"amdgcn-amd-amdhsa--gfx950" in open(path, "rb").read()
+    assert not hasattr(_lib.lib(), "cxm_timeline_read")
