@@ -77,10 +77,11 @@ def parse():
     p.add_argument("--copy-calibration", action="store_true",
                    help="first copy 64 MiB device-to-device three times (the known-size "
                         "kernel that scales FETCH_SIZE / WRITE_SIZE counters)")
-    p.add_argument("--timeline", action="store_true",
-                   help="instead of the bench line, print per-workgroup timelines of the C2 row sum, column sum, "
-                        "global sum and column argmax from the diagnostics build cortexmind_amd/"
-                        "libcxm_hip_timeline.so (make -C cortexmind_amd/csrc timeline)")
+    p.add_argument("--timeline", nargs="?", const="c2", choices=["c2", "c5"],
+                   help="instead of the bench line, print per-workgroup timelines from the diagnostics build "
+                        "cortexmind_amd/libcxm_hip_timeline.so (make -C cortexmind_amd/csrc timeline): c2 (default) "
+                        "the C2 row sum, column sum, global sum and column argmax; c5 the MLP step's ring "
+                        "products and output-layer head")
     p.add_argument("--summarize", nargs="+", metavar=("KIND", "CSV"),
                    help="summarise rocprofv3 output instead of running: 'trace <kernel_trace.csv>' prints the "
                         "per-kernel table of profiles/*_kernel_trace.md; 'pmc <counter_collection.csv>...' prints "
@@ -285,6 +286,94 @@ def timeline_report(t, ops, grids):
         xcd = np.arange(r.shape[0]) % 8
         per = [(r[xcd == c, 1].max() - ln[9]) / 100.0 for c in range(8)]
         print(f"| {name} | " + " ".join(f"{v:.2f}" for v in per) + " |")
+
+
+GEMM_TL = (4, 1024, 6)  # gemm.hip's ring tables: instances, workgroups, marks
+HEAD_TL = (256, 8)  # mlp.hip's head table
+
+
+def timeline_mlp(steps=40):
+    """`steps` C5 MLP steps back to back, then the diagnostics build's marks
+    of the last step: per ring product (0 entry, 1 prologue done: the first
+    four stages landed, 2 K loop done, 3 epilogue done; 4 and 5 the core
+    clock counter at 1 and 2) and per head workgroup (0 entry, 1 W3 and h2
+    loaded, 2 W3 in LDS, 3 logits, 4 cross-entropy, 5 dh2 stored, 6 partials
+    stored), in us from the step's first workgroup start."""
+    import ctypes
+
+    from cortexmind_amd import _lib
+
+    _lib.LIB_PATH = os.path.join(ROOT, "cortexmind_amd", "libcxm_hip_timeline.so")
+    from cortexmind_amd import engine as E
+    from cortexmind_amd._lib import call, lib
+    from cortexmind_amd.data import c5_mlp
+    from cortexmind_amd.device import DeviceArray as D
+
+    x, labels, params = c5_mlp()
+    B, d0 = x.shape
+    d1, d2, d3 = params["w1"].shape[1], params["w2"].shape[1], params["w3"].shape[1]
+    dx_, dl_ = D.from_numpy(x), D.from_numpy(labels)
+    P = {k: D.from_numpy(v) for k, v in params.items()}
+    loss = D((1,))
+    net = E.Mlp3(B, d0, d1, d2, d3)
+    for _ in range(steps):
+        net.step(dx_, dl_, P, 0.01, loss)
+    call("cxm_device_sync")
+    g = np.zeros(GEMM_TL, np.uint64)
+    h = np.zeros(HEAD_TL, np.uint64)
+    for name, arr in (("cxm_timeline_gemm_read", g), ("cxm_timeline_head_read", h)):
+        fn = getattr(lib(), name)
+        fn.argtypes, fn.restype = [ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int
+        if fn(arr.ctypes.data, arr.size) != 0:
+            raise RuntimeError(f"{name} failed")
+    timeline_mlp_report(g, h, {0: 256, 1: 256, 2: 256, 3: 240}, 256)
+
+
+def timeline_mlp_report(g, h, wgs, head_wgs):
+    """Prints timeline_mlp()'s table from the raw marks: g [instances, wgs,
+    marks] of the ring products (`wgs` product workgroups per instance), h
+    [head workgroups, marks]."""
+    g, h = g.astype(np.int64), h.astype(np.int64)
+    names = {0: ("layer-1 forward", "k_gemm_ring<true,false,true>"), 1: ("layer-2 forward", "k_gemm_ring<true,false,false>"),
+             2: ("layer-2 input gradient", "k_gemm_ring<true,true,false>"),
+             3: ("weight gradients, paired", "k_gemm_ring_pair<false,false>")}
+    rec = {k: g[k, :n] for k, n in wgs.items()}
+    hd = h[:head_wgs]
+    t0 = min(int(r[:, 0].min()) for r in rec.values())
+    us = lambda v: (np.asarray(v, dtype=np.float64) - t0) / 100.0  # noqa: E731
+    rows = []
+    for k in (0, 1):
+        rows.append((k, rec[k]))
+    rows.append(("head", hd))
+    rows += [(2, rec[2]), (3, rec[3])]
+    print("| kernel | workgroups | first start | last start | prologue (median) | K loop (median / max) | "
+          "epilogue (median / max) | end | core clock in the K loop, GHz (median) | gap to the next kernel |")
+    print("|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|")
+    spans = []
+    for k, r in rows:
+        if k == "head":
+            spans.append((r[:, 0].min(), r[:, 6].max()))
+        else:
+            spans.append((r[:, 0].min(), r[:, 3].max()))
+    for i, (k, r) in enumerate(rows):
+        gap = (spans[i + 1][0] - spans[i][1]) / 100.0 if i + 1 < len(rows) else None
+        gs = f"{gap:.2f}" if gap is not None else "—"
+        if k == "head":
+            print(f"| output-layer head (`k_mlp_head`) | {r.shape[0]} | {us(r[:, 0].min()):.2f} | {us(r[:, 0].max()):.2f} | "
+                  f"— | — | — | {us(r[:, 6].max()):.2f} | — | {gs} |")
+            continue
+        pro, loop, epi = (r[:, 1] - r[:, 0]) / 100.0, (r[:, 2] - r[:, 1]) / 100.0, (r[:, 3] - r[:, 2]) / 100.0
+        clk = (r[:, 5] - r[:, 4]) / np.maximum(r[:, 2] - r[:, 1], 1) / 10.0  # counter ticks per 10 ns -> GHz
+        print(f"| {names[k][0]} (`{names[k][1]}`) | {r.shape[0]} | {us(r[:, 0].min()):.2f} | {us(r[:, 0].max()):.2f} | "
+              f"{np.median(pro):.2f} | {np.median(loop):.2f} / {loop.max():.2f} | {np.median(epi):.2f} / {epi.max():.2f} | "
+              f"{us(r[:, 3].max()):.2f} | {np.median(clk):.3f} | {gs} |")
+    print()
+    marks = ["W3 and h2 loaded", "W3 in LDS", "logits", "cross-entropy", "dh2 stored", "partials stored"]
+    print("| output-layer head phase | median | last |")
+    print("|---|---:|---:|")
+    for i, m in enumerate(marks, start=1):
+        d = (hd[:, i] - hd[:, 0]) / 100.0
+        print(f"| {m} (us after the workgroup's start) | {np.median(d):.2f} | {d.max():.2f} |")
 
 
 class Op:
@@ -884,8 +973,11 @@ def main():
     if args.summarize:
         summarize(args.summarize[0], args.summarize[1:])
         return
-    if args.timeline:
+    if args.timeline == "c2":
         timeline()
+        return
+    if args.timeline == "c5":
+        timeline_mlp()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on one GPU only (every GPU box here has one); "

@@ -25,6 +25,31 @@
 #include "cxm_common.hpp"
 #include "mlp_side.hpp"
 
+// Per-workgroup timeline of the ring products, for the diagnostics build only
+// (this file compiled with -DCXM_TIMELINE into libcxm_hip_timeline.so,
+// read by `bench.py --timeline c5`).  Thread 0 of a workgroup writes the
+// 100 MHz s_memrealtime clock to mark i of its record: 0 entry, 1 the
+// first four ring stages landed (prologue done), 2 the K loop done, 3 the
+// epilogue done (past a barrier, so every wave's stores are issued); marks
+// 4 and 5 hold the core-clock counter s_memtime at marks 1 and 2.  Table
+// by instance: 0 the K-tail instance, 1 A.B, 2 A.B^T, 3 the other forms
+// (the paired weight gradients' A^T.B).  Records are indexed by blockIdx.x
+// modulo kGemmTlWgs; a launch overwrites the previous records of its
+// instance.  Without CXM_TIMELINE the marks compile to nothing.
+#ifdef CXM_TIMELINE
+constexpr unsigned kGemmTlKinds = 4, kGemmTlWgs = 1024, kGemmTlMarks = 6;
+static __device__ unsigned long long gemm_timeline[kGemmTlKinds][kGemmTlWgs][kGemmTlMarks];
+__device__ __forceinline__ void gemm_tl_mark(unsigned kind, unsigned i) {
+    if (threadIdx.x == 0) {
+        unsigned long long *rec = gemm_timeline[kind][blockIdx.x % kGemmTlWgs];
+        __builtin_nontemporal_store(__builtin_amdgcn_s_memrealtime(), &rec[i]);
+        if (i == 1 || i == 2) __builtin_nontemporal_store(__builtin_amdgcn_s_memtime(), &rec[3 + i]);
+    }
+}
+#else
+__device__ __forceinline__ void gemm_tl_mark(unsigned, unsigned) {}
+#endif
+
 namespace cxm {
 namespace {
 
@@ -907,6 +932,8 @@ __device__ __forceinline__ void ring_gemm(const float *__restrict__ A, const flo
                                           float *__restrict__ part, unsigned *__restrict__ counters, unsigned wg) {
     __shared__ __attribute__((aligned(16))) float s0[2 * kRST], s1[2 * kRST], s2[2 * kRST], s3[2 * kRST];
     __shared__ int flag;
+    constexpr unsigned tl_kind = TAIL ? 0u : (KCA && !KCB) ? 1u : (KCA && KCB) ? 2u : 3u;
+    gemm_tl_mark(tl_kind, 0);
     const unsigned tile = wg / splits;
     const unsigned split = wg - tile * splits;
     const size_t m0 = static_cast<size_t>(tile / tiles_n) * BM;
@@ -945,6 +972,7 @@ __device__ __forceinline__ void ring_gemm(const float *__restrict__ A, const flo
     ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, kt(2), kl, L, s2);
     ring_fill_any<KCA, KCB, TAIL>(A, B, lda, ldb, m0, n0, kt(3), kl, L, s3);
     ring_barrier<3 * kRPS>();
+    gemm_tl_mark(tl_kind, 1);
     RingFrag f0;
     ring_frags<KCA, KCB>(s0, 0, wm, wn, l32, lhi, f0);
 #define CXM_RING_STEP(T4, CUR, NXT) \
@@ -986,7 +1014,12 @@ __device__ __forceinline__ void ring_gemm(const float *__restrict__ A, const flo
     }
 #undef CXM_RING_STEP
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
+    gemm_tl_mark(tl_kind, 2);
     gemm_epilogue<2, 2>(acc, C, M, N, m0, n0, tile, split, splits, wm, wn, lhi, l32, epi, part, counters, &flag);
+#ifdef CXM_TIMELINE
+    __syncthreads();
+    gemm_tl_mark(tl_kind, 3);
+#endif
 }
 
 template <bool KCA, bool KCB, bool TAIL>
@@ -1524,6 +1557,17 @@ int gemm_ex_pair(const GemmSpec &a, const GemmSpec &b, cxm_stream_t st, StepSide
 }
 
 }  // namespace cxm
+
+#ifdef CXM_TIMELINE
+// Diagnostics build only (not declared in include/cxm_hip.h): copies the
+// ring products' timeline tables (kGemmTlKinds x kGemmTlWgs x kGemmTlMarks
+// 64-bit words) to host memory, after the caller's synchronisation.
+extern "C" int cxm_timeline_gemm_read(unsigned long long *host, size_t words) {
+    if (!host || words != static_cast<size_t>(kGemmTlKinds) * kGemmTlWgs * kGemmTlMarks) return CXM_E_INVALID;
+    const hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(gemm_timeline), words * sizeof(unsigned long long));
+    return e == hipSuccess ? CXM_OK : static_cast<int>(e);
+}
+#endif
 
 extern "C" {
 

@@ -85,6 +85,24 @@ __host__ __device__ inline size_t head_part_width(size_t d2, size_t d3) { return
 constexpr int kWkStride = 20;
 constexpr int kHeadW3PerThread = kHeadMaxD2 * 16 / kHeadThreads;
 
+// Per-workgroup timeline of the head, for the diagnostics build only (this
+// file compiled with -DCXM_TIMELINE, read by `bench.py --timeline c5`):
+// thread 0 writes the 100 MHz s_memrealtime clock to mark i of record
+// blockIdx.x % kHeadTlWgs: 0 entry, 1 W3 and h2 loaded (first barrier),
+// 2 W3 in LDS, 3 logits, 4 cross-entropy, 5 dh2 stored and summed, 6 the
+// partials stored (past a final barrier).  Without CXM_TIMELINE the marks
+// compile to nothing.
+#ifdef CXM_TIMELINE
+constexpr unsigned kHeadTlWgs = 256, kHeadTlMarks = 8;
+static __device__ unsigned long long head_timeline[kHeadTlWgs][kHeadTlMarks];
+__device__ __forceinline__ void head_tl_mark(unsigned i) {
+    if (threadIdx.x == 0)
+        __builtin_nontemporal_store(__builtin_amdgcn_s_memrealtime(), &head_timeline[blockIdx.x % kHeadTlWgs][i]);
+}
+#else
+__device__ __forceinline__ void head_tl_mark(unsigned) {}
+#endif
+
 __device__ __forceinline__ float row16_sum(float v) {  // sum over the 16-lane row, in every lane of it
     v += dpp<kQuadXor1>(v);
     v += dpp<kQuadXor2>(v);
@@ -114,6 +132,7 @@ __global__ __launch_bounds__(kHeadThreads) void k_mlp_head(const float *__restri
     __shared__ float nl[16];
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave, tid = threadIdx.x;
     const int l16 = lane & 15, q = lane >> 4;
+    head_tl_mark(0);
     const int nc = static_cast<int>(D3), d2 = static_cast<int>(D2), nw3 = d2 * nc;
     const size_t r0 = static_cast<size_t>(blockIdx.x) * kHeadRows;
     // Every load is issued as straight-line code from a clamped, in-range
@@ -142,6 +161,7 @@ __global__ __launch_bounds__(kHeadThreads) void k_mlp_head(const float *__restri
         for (int c4 = 0; c4 < kWkStride / 4; ++c4) row[c4] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
+    head_tl_mark(1);
     const float rnc = 1.0f / static_cast<float>(nc);
 #pragma unroll
     for (int j = 0; j < kHeadW3PerThread; ++j) {
@@ -152,6 +172,7 @@ __global__ __launch_bounds__(kHeadThreads) void k_mlp_head(const float *__restri
         if (i < nw3) Wk[k * kWkStride + c] = wt[j];
     }
     __syncthreads();
+    head_tl_mark(2);
 
     // 1. partial logits over this wave's 64 k (two accumulators, added at the end)
     f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
@@ -169,6 +190,7 @@ __global__ __launch_bounds__(kHeadThreads) void k_mlp_head(const float *__restri
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[w][4 * q + i][l16] = acc0[i] + acc1[i];
     __syncthreads();
+    head_tl_mark(3);
 
     // 2. cross-entropy in waves 0..3: lane (row 4 w + q, class l16)
     if (w < 4) {
@@ -190,6 +212,7 @@ __global__ __launch_bounds__(kHeadThreads) void k_mlp_head(const float *__restri
         if (l16 == 0) nl[row] = valid ? (ok ? nll : NAN) : 0.0f;
     }
     __syncthreads();
+    head_tl_mark(4);
 
     // 3. dh2 = (dl W3^T) * [h2 > 0] through dh2^T = W3 dl^T, and its column sums
     const float4 bd = *reinterpret_cast<const float4 *>(&dt[l16][4 * q]);  // dl[l16][4 q .. + 3]
@@ -231,6 +254,7 @@ __global__ __launch_bounds__(kHeadThreads) void k_mlp_head(const float *__restri
     for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[blk][i] += dpp<kRowMirror>(o[blk][i]);
+    head_tl_mark(5);
     float *__restrict__ prow = part + static_cast<size_t>(blockIdx.x) * head_part_width(D2, D3);
 
     // 4. gW3 over the 16 rows, G[k][c] = sum_b h2[b][k] dl[b][c], on the same MFMA with the
@@ -273,6 +297,10 @@ __global__ __launch_bounds__(kHeadThreads) void k_mlp_head(const float *__restri
         for (int r = 0; r < 16; ++r) t += nl[r];
         prow[D2] = t;
     }
+#ifdef CXM_TIMELINE
+    __syncthreads();
+    head_tl_mark(6);
+#endif
 }
 
 // Column c of the partials: the sum over workgroups p = q, q + 16, ... per
@@ -344,6 +372,17 @@ int run_head_finish(const cxm_mlp3 *h, float *w3, float *b3, float *b2, float lr
 
 }  // namespace
 }  // namespace cxm
+
+#ifdef CXM_TIMELINE
+// Diagnostics build only (not declared in include/cxm_hip.h): copies the
+// head's timeline table (kHeadTlWgs x kHeadTlMarks 64-bit words) to host
+// memory, after the caller's synchronisation.
+extern "C" int cxm_timeline_head_read(unsigned long long *host, size_t words) {
+    if (!host || words != static_cast<size_t>(cxm::kHeadTlWgs) * cxm::kHeadTlMarks) return CXM_E_INVALID;
+    const hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(cxm::head_timeline), words * sizeof(unsigned long long));
+    return e == hipSuccess ? CXM_OK : static_cast<int>(e);
+}
+#endif
 
 extern "C" {
 

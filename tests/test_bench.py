@@ -140,3 +140,30 @@ def test_timeline_report_on_synthetic_marks(capsys):
     assert row[9].strip() == "2.00"    # gap to the column op: 200 ticks
     assert col[7].strip() == f"{(c0 + 1300 - base) / 100:.2f}"
     assert col[8].strip() == "2.93"    # combine after the last fold: 1300 - 1007 ticks
+
+
+def test_timeline_mlp_report_on_synthetic_marks(capsys):
+    """timeline_mlp_report: prologue / loop / epilogue from the marks, the
+    core clock from the s_memtime ticks over the loop's 10 ns ticks, gaps
+    from one kernel's last epilogue to the next kernel's first start."""
+    sys.path.insert(0, ROOT)
+    import numpy as np
+
+    from bench import GEMM_TL, HEAD_TL, timeline_mlp_report
+
+    g = np.zeros(GEMM_TL, np.uint64)
+    h = np.zeros(HEAD_TL, np.uint64)
+    t = 1000
+    for k in range(4):
+        for w in range(8):
+            g[k, w] = [t, t + 150, t + 5150, t + 5600, 7, 7 + 5000 * 23]  # 50 us loop at 2.3 GHz
+        t += 6000 if k != 1 else 8000  # the head runs between the second and third product
+    for w in range(4):
+        h[w] = [13100, 13400, 13500, 13600, 13700, 13900, 14300, 0]
+    timeline_mlp_report(g, h, {0: 8, 1: 8, 2: 8, 3: 8}, 4)
+    out = capsys.readouterr().out.splitlines()
+    l1 = [ln for ln in out if ln.startswith("| layer-1 forward")][0].split("|")
+    assert [c.strip() for c in l1[3:11]] == ["0.00", "0.00", "1.50", "50.00 / 50.00", "4.50 / 4.50", "56.00", "2.300",
+                                             "4.00"]
+    hd = [ln for ln in out if ln.startswith("| output-layer head (")][0].split("|")
+    assert hd[3].strip() == "121.00" and hd[8].strip() == "133.00" and hd[10].strip() == "7.00"
