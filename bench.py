@@ -77,11 +77,11 @@ def parse():
     p.add_argument("--copy-calibration", action="store_true",
                    help="first copy 64 MiB device-to-device three times (the known-size "
                         "kernel that scales FETCH_SIZE / WRITE_SIZE counters)")
-    p.add_argument("--timeline", nargs="?", const="c2", choices=["c2", "c5"],
+    p.add_argument("--timeline", nargs="?", const="c2", choices=["c2", "c4", "c5"],
                    help="instead of the bench line, print per-workgroup timelines from the diagnostics build "
                         "cortexmind_amd/libcxm_hip_timeline.so (make -C cortexmind_amd/csrc timeline): c2 (default) "
-                        "the C2 row sum, column sum, global sum and column argmax; c5 the MLP step's ring "
-                        "products and output-layer head")
+                        "the C2 row sum, column sum, global sum and column argmax; c4 the long-row softmax and "
+                        "log-softmax, forward and backward; c5 the MLP step's ring products and output-layer head")
     p.add_argument("--summarize", nargs="+", metavar=("KIND", "CSV"),
                    help="summarise rocprofv3 output instead of running: 'trace <kernel_trace.csv>' prints the "
                         "per-kernel table of profiles/*_kernel_trace.md; 'pmc <counter_collection.csv>...' prints "
@@ -286,6 +286,71 @@ def timeline_report(t, ops, grids):
         xcd = np.arange(r.shape[0]) % 8
         per = [(r[xcd == c, 1].max() - ln[9]) / 100.0 for c in range(8)]
         print(f"| {name} | " + " ".join(f"{v:.2f}" for v in per) + " |")
+
+
+SM_TL = (4, 1024, 5)  # softmax.hip's long-row tables: kernels, workgroups, marks
+
+
+def timeline_softmax(reps=40):
+    """C4's softmax and log-softmax, forward and backward, [64, 131072], back
+    to back `reps` times (inputs rotating over four sets), then the
+    diagnostics build's marks of the last round: 0 entry, 1 (forward only)
+    its staggered start over, 2 partial published, 3 the row's partials in,
+    4 stores issued; in us from the round's first start."""
+    import ctypes
+
+    from cortexmind_amd import _lib
+
+    _lib.LIB_PATH = os.path.join(ROOT, "cortexmind_amd", "libcxm_hip_timeline.so")
+    from cortexmind_amd import engine as E
+    from cortexmind_amd._lib import call, lib
+    from cortexmind_amd.data import c4_long_softmax
+    from cortexmind_amd.device import DeviceArray as D
+
+    x, dy = c4_long_softmax()
+    r, c = x.shape
+    nset = 4
+    X = [D.from_numpy(x) for _ in range(nset)]
+    G = [D.from_numpy(dy) for _ in range(nset)]
+    Y = [D((r, c)) for _ in range(nset)]
+    dX = [D((r, c)) for _ in range(nset)]
+    S = E.softmax
+    ops = [("softmax fwd", "k_sm_fwd_x<false>", 0, lambda k: S.forward(X[k], Y[k], r, c)),
+           ("log-softmax fwd", "k_sm_fwd_x<true>", 1, lambda k: S.forward(X[k], Y[k], r, c, log=True)),
+           ("softmax bwd", "k_sm_bwd_x<false>", 2, lambda k: S.backward(Y[k], G[k], dX[k], r, c)),
+           ("log-softmax bwd", "k_sm_bwd_x<true>", 3, lambda k: S.backward(Y[k], G[k], dX[k], r, c, log=True))]
+    for i in range(reps):
+        for _, _, _, fn in ops:
+            fn(i % nset)
+    call("cxm_device_sync")
+    t = np.zeros(SM_TL, np.uint64)
+    fn = lib().cxm_timeline_softmax_read
+    fn.argtypes, fn.restype = [ctypes.c_void_p, ctypes.c_size_t], ctypes.c_int
+    if fn(t.ctypes.data, t.size) != 0:
+        raise RuntimeError("cxm_timeline_softmax_read failed")
+    timeline_softmax_report(t, [(n, k, kind) for n, k, kind, _ in ops], r * (c // 8192))
+
+
+def timeline_softmax_report(t, ops, wgs):
+    """Prints timeline_softmax()'s table from the raw marks t [kernels, wgs,
+    marks]; `ops` lists (name, kernel, table) in launch order."""
+    t = t.astype(np.int64)
+    recs = {kind: t[kind, :wgs] for _, _, kind in ops}
+    t0 = min(int(r[:, 0].min()) for r in recs.values())
+    us = lambda v: (np.asarray(v, dtype=np.float64) - t0) / 100.0  # noqa: E731
+    print("| op (kernel) | workgroups | first start | last start | staggered start over: last | first workgroup done | "
+          "partial published: median / last | row's partials in: median / last | "
+          "exchange wait per workgroup: median / max | end | gap to the next op |")
+    print("|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|")
+    for i, (name, kern, kind) in enumerate(ops):
+        r = recs[kind]
+        wait = (r[:, 3] - r[:, 2]) / 100.0
+        end = r[:, 4].max()
+        gap = (recs[ops[i + 1][2]][:, 0].min() - end) / 100.0 if i + 1 < len(ops) else None
+        print(f"| {name} (`{kern}`) | {r.shape[0]} | {us(r[:, 0].min()):.2f} | {us(r[:, 0].max()):.2f} | "
+              + (f"{us(r[:, 1].max()):.2f}" if r[:, 1].max() > 0 else "—") + f" | {us(r[:, 4].min()):.2f} | "
+              f"{us(np.median(r[:, 2])):.2f} / {us(r[:, 2].max()):.2f} | {us(np.median(r[:, 3])):.2f} / {us(r[:, 3].max()):.2f} | "
+              f"{np.median(wait):.2f} / {wait.max():.2f} | {us(end):.2f} | " + (f"{gap:.2f}" if gap is not None else "—") + " |")
 
 
 GEMM_TL = (4, 1024, 6)  # gemm.hip's ring tables: instances, workgroups, marks
@@ -978,6 +1043,9 @@ def main():
         return
     if args.timeline == "c5":
         timeline_mlp()
+        return
+    if args.timeline == "c4":
+        timeline_softmax()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on one GPU only (every GPU box here has one); "

@@ -29,6 +29,29 @@
 
 #include "cxm_common.hpp"
 
+// Per-workgroup timeline of the single-pass long-row kernels, for the
+// diagnostics build only (this file compiled with -DCXM_TIMELINE into
+// libcxm_hip_timeline.so, read by `bench.py --timeline c4`).  Thread 0 of a
+// workgroup writes the 100 MHz s_memrealtime clock to mark i of its
+// record: 0 entry, 1 (forward only) its staggered start over, 2 its
+// partial reduced and published, 3 the row's partials in
+// (past the barrier after the exchange), 4 its stores issued (past a final
+// barrier).  Tables: 0 softmax forward, 1 log-softmax forward, 2 softmax
+// backward, 3 log-softmax backward; records indexed by the linear
+// workgroup id modulo kSmTlWgs, overwritten by the next launch of the same
+// table.  Without CXM_TIMELINE the marks compile to nothing.
+#ifdef CXM_TIMELINE
+constexpr unsigned kSmTlKinds = 4, kSmTlWgs = 1024, kSmTlMarks = 5;
+static __device__ unsigned long long sm_timeline[kSmTlKinds][kSmTlWgs][kSmTlMarks];
+__device__ __forceinline__ void sm_tl_mark(unsigned kind, unsigned i) {
+    if (threadIdx.x == 0)
+        __builtin_nontemporal_store(__builtin_amdgcn_s_memrealtime(),
+                                    &sm_timeline[kind][(blockIdx.x + gridDim.x * blockIdx.y) % kSmTlWgs][i]);
+}
+#else
+__device__ __forceinline__ void sm_tl_mark(unsigned, unsigned) {}
+#endif
+
 namespace cxm {
 namespace {
 
@@ -488,7 +511,10 @@ __global__ __launch_bounds__(kBlock) void k_sm_fwd_x(const float *__restrict__ x
     __shared__ unsigned long long s_miss;
     // grid (segs, rows): no division ahead of the loads
     const unsigned seg = blockIdx.x, row = blockIdx.y;
+    constexpr unsigned tl = LOG ? 1u : 0u;
+    sm_tl_mark(tl, 0);
     x_stagger(row, gmul, quanta);
+    sm_tl_mark(tl, 1);
     unsigned *h = hdr + row * kCtr;
     const unsigned tag = x_epoch(h) + 1;  // every wave: a load behind a branch would be waited for at its end
     const float *__restrict__ xr = x + static_cast<size_t>(row) * cols;
@@ -520,11 +546,13 @@ __global__ __launch_bounds__(kBlock) void k_sm_fwd_x(const float *__restrict__ x
         part[0][seg] = Mb;
         part[1][seg] = Sb;
     }
+    sm_tl_mark(tl, 2);
     if (threadIdx.x < kWave) {
         const unsigned long long miss = x_gather<2>(sl, segs, seg, tag, limit, part);
         if (threadIdx.x == 0) s_miss = miss;
     }
     __syncthreads();
+    sm_tl_mark(tl, 3);
     // peers not seen: recompute their partials from the input, same arithmetic
     for (unsigned long long miss = s_miss; miss; miss &= miss - 1) {
         const unsigned b = static_cast<unsigned>(__builtin_ctzll(miss));
@@ -573,6 +601,10 @@ __global__ __launch_bounds__(kBlock) void k_sm_fwd_x(const float *__restrict__ x
         }
     }
     if (threadIdx.x == 0) x_leave(h, ticket, segs, tag);
+#ifdef CXM_TIMELINE
+    __syncthreads();
+    sm_tl_mark(tl, 4);
+#endif
 }
 
 // Backward: partial r_b = sum(dy*y) or sum(dy) per segment, r = sum_b r_b
@@ -587,6 +619,8 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_x(const float *__restrict__ y
     __shared__ float part[1][kXMaxSegs];
     __shared__ unsigned long long s_miss;
     const unsigned seg = blockIdx.x, row = blockIdx.y;  // grid (segs, rows)
+    constexpr unsigned tl = LOG ? 3u : 2u;
+    sm_tl_mark(tl, 0);
     unsigned *h = hdr + row * kCtr;
     const unsigned tag = x_epoch(h) + 1;  // every wave: a load behind a branch would be waited for at its end
     const size_t rbase = static_cast<size_t>(row) * cols;
@@ -611,11 +645,13 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_x(const float *__restrict__ y
         ticket = x_ticket(h);
         part[0][seg] = rb;
     }
+    sm_tl_mark(tl, 2);
     if (threadIdx.x < kWave) {
         const unsigned long long miss = x_gather<1>(sl, segs, seg, tag, limit, part);
         if (threadIdx.x == 0) s_miss = miss;
     }
     __syncthreads();
+    sm_tl_mark(tl, 3);
     for (unsigned long long miss = s_miss; miss; miss &= miss - 1) {
         const unsigned b = static_cast<unsigned>(__builtin_ctzll(miss));
         const size_t bb = rbase + b * kXSeg;
@@ -649,6 +685,10 @@ __global__ __launch_bounds__(kBlock) void k_sm_bwd_x(const float *__restrict__ y
         st4_stream(dx + base + 4 * i, o);
     }
     if (threadIdx.x == 0) x_leave(h, ticket, segs, tag);
+#ifdef CXM_TIMELINE
+    __syncthreads();
+    sm_tl_mark(tl, 4);
+#endif
 }
 
 // --------------------------------------------------- generic (any shape)
@@ -952,6 +992,17 @@ int softmax_bwd(const float *y, const float *dy, float *dx, size_t rows, size_t 
 
 }  // namespace
 }  // namespace cxm
+
+#ifdef CXM_TIMELINE
+// Diagnostics build only (not declared in include/cxm_hip.h): copies the
+// long-row softmax timeline tables (kSmTlKinds x kSmTlWgs x kSmTlMarks 64-bit
+// words) to host memory, after the caller's synchronisation.
+extern "C" int cxm_timeline_softmax_read(unsigned long long *host, size_t words) {
+    if (!host || words != static_cast<size_t>(kSmTlKinds) * kSmTlWgs * kSmTlMarks) return CXM_E_INVALID;
+    const hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(sm_timeline), words * sizeof(unsigned long long));
+    return e == hipSuccess ? CXM_OK : static_cast<int>(e);
+}
+#endif
 
 using namespace cxm;
 

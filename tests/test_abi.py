@@ -128,7 +128,7 @@ def test_pool_core_bookkeeping():
 
 
 def test_timeline_build_exports_its_reader():
-    """The diagnostics build (reduce.hip, gemm.hip and mlp.hip with
+    """The diagnostics build (reduce.hip, softmax.hip, gemm.hip and mlp.hip with
     -DCXM_TIMELINE, built beside the library) carries gfx950 code and exports
     its table readers; the library itself does not."""
     import os
@@ -137,8 +137,8 @@ def test_timeline_build_exports_its_reader():
     if not os.path.exists(path):
         pytest.skip("diagnostics build not built (make -C cortexmind_amd/csrc timeline)")
     tl = ctypes.CDLL(path)
-    for name in ("cxm_timeline_read", "cxm_timeline_gemm_read", "cxm_timeline_head_read"):
+    for name in ("cxm_timeline_read", "cxm_timeline_softmax_read", "cxm_timeline_gemm_read", "cxm_timeline_head_read"):
         assert hasattr(tl, name), name
     assert b"amdgcn-amd-amdhsa--gfx950" in open(path, "rb").read()
-    assert not any(hasattr(_lib.lib(), n) for n in ("cxm_timeline_read", "cxm_timeline_gemm_read",
-                                                    "cxm_timeline_head_read"))
+    assert not any(hasattr(_lib.lib(), n) for n in ("cxm_timeline_read", "cxm_timeline_softmax_read",
+                                                    "cxm_timeline_gemm_read", "cxm_timeline_head_read"))

@@ -167,3 +167,21 @@ def test_timeline_mlp_report_on_synthetic_marks(capsys):
                                              "4.00"]
     hd = [ln for ln in out if ln.startswith("| output-layer head (")][0].split("|")
     assert hd[3].strip() == "121.00" and hd[8].strip() == "133.00" and hd[10].strip() == "7.00"
+
+
+def test_timeline_softmax_report_on_synthetic_marks(capsys):
+    sys.path.insert(0, ROOT)
+    import numpy as np
+
+    from bench import SM_TL, timeline_softmax_report
+
+    t = np.zeros(SM_TL, np.uint64)
+    for k in range(2):
+        for w in range(16):
+            b = 1000 + 2000 * k
+            t[k, w] = [b + w, b + 10 + w, b + 900, b + 950 + (w % 2) * 100, b + 1500]
+    timeline_softmax_report(t, [("fwd", "k_f", 0), ("bwd", "k_b", 1)], 16)
+    out = capsys.readouterr().out.splitlines()
+    f = [ln for ln in out if ln.startswith("| fwd")][0].split("|")
+    assert [c.strip() for c in f[3:12]] == ["0.00", "0.15", "0.25", "15.00", "9.00 / 9.00", "10.00 / 10.50",
+                                            "1.00 / 1.50", "15.00", "5.00"]
