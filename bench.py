@@ -88,7 +88,8 @@ def parse():
                         "per-kernel FETCH_SIZE / WRITE_SIZE bytes per launch scaled by the 64 MiB copy "
                         "(profiles/pmc_traffic.txt lines); 'mfma <counter_collection.csv>' prints per-kernel "
                         "MFMA busy from SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_MFMA and GRBM_GUI_ACTIVE; 'tcc <counter_collection.csv>' "
-                        "per-kernel L2 hits and misses from TCC_HIT_sum and TCC_MISS_sum")
+                        "per-kernel L2 hits and misses from TCC_HIT_sum and TCC_MISS_sum; 'counters <counter_collection.csv>' "
+                        "every counter's mean per dispatch")
     return p.parse_args()
 
 
@@ -149,6 +150,26 @@ def summarize(kind, paths):
                 continue
             # GRBM_GUI_ACTIVE sums the 8 XCDs' busy cycles; 1024 SIMDs in all
             print(f"| `{k}` | {grid} | {len(cs)} | {ga / len(cs) / 8:.3g} | {mb / mi:.0f} | {100 * mb / (ga / 8 * 1024):.1f}% |")
+        return
+    if kind == "counters":
+        # every counter of the CSV, mean per dispatch, per kernel and grid
+        disp, meta, names = {}, {}, []
+        for r in csv.DictReader(open(paths[0])):
+            k = int(r["Dispatch_Id"])
+            disp.setdefault(k, {})[r["Counter_Name"]] = float(r["Counter_Value"])
+            meta[k] = (kernel_name(r["Kernel_Name"]), int(r["Grid_Size"]))
+            if r["Counter_Name"] not in names:
+                names.append(r["Counter_Name"])
+        g = OrderedDict()
+        for k, c in disp.items():
+            g.setdefault(meta[k], []).append(c)
+        print("| kernel | grid (threads) | dispatches | " + " | ".join(names) + " |")
+        print("|---|---:|---:|" + "---:|" * len(names))
+        for (k, grid), cs in sorted(g.items(), key=lambda kv: kv[0]):
+            if k.startswith("__amd_rocclr"):
+                continue
+            vals = [sum(c.get(n, 0.0) for c in cs) / len(cs) for n in names]
+            print(f"| `{k}` | {grid} | {len(cs)} | " + " | ".join(f"{v:.4g}" for v in vals) + " |")
         return
     if kind == "tcc":
         disp, meta = {}, {}
